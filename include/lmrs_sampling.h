@@ -1,0 +1,124 @@
+/*
+ * lmrs_sampling.h -- C-ABI of the MI355X batched token sampler.
+ *
+ * One call samples one token for each of `batch` rows of a [batch, vocab]
+ * logits tensor that already lives in device memory.  It replaces, for a whole
+ * decode step, the reference's per-row `Sampler::sample`
+ * (crates/sampling/src/sampler/sampler.rs:178-186): the processor chain
+ * (RepetitionPenalty crates/sampling/src/logits/repetition.rs:80-117,
+ * FrequencyPresencePenalty logits/presence.rs:100-130, Temperature
+ * logits/temperature.rs:66-72, each a chain of CUDA elementwise kernels bound
+ * through crates/kernels/src/tensor_ops.rs:28-34,142-174), the cast and copy
+ * to the host (tensor_ops.rs:176-186), and the host strategy (Greedy / TopK /
+ * TopP / softmax_choice, crates/sampling/src/strategies/mod.rs:21-61,
+ * greedy.rs:22-29, top_k.rs:39-45, top_p.rs:39-61).
+ *
+ * Conventions follow the reference's native layer (kernels/ffi, declared in
+ * crates/kernels/src/raw.rs:53-147): plain pointers and sizes, dtype codes
+ * 0 = bf16, 1 = f16, 2 = f32 (raw.rs:9-14), stream last.  Two deliberate
+ * differences: calls return a status instead of void, so bad arguments are
+ * never silently ignored (the reference's *_fwd ignore an unknown dtype,
+ * ops_ffi.cu:72-79), and per-row failures are reported in `status[r]`
+ * instead of a Rust Result.
+ *
+ * Everything is asynchronous on `stream` (a hipStream_t; NULL = the null
+ * stream).  No call allocates device memory.  All device pointers must stay
+ * valid until the stream reaches the call.
+ */
+#ifndef LMRS_SAMPLING_H
+#define LMRS_SAMPLING_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes (crates/kernels/src/raw.rs:9-14). f16 is not accepted by the
+ * sampler: the reference Sampler takes bf16 only (tensor_ops.rs:177); f32 is
+ * accepted and processed without bf16 rounding. */
+#define LMRS_DTYPE_BF16 0
+#define LMRS_DTYPE_F16 1
+#define LMRS_DTYPE_F32 2
+
+/* Return codes of the entry points. */
+#define LMRS_OK 0
+#define LMRS_ERR_NULL_ARGUMENT -1  /* a required pointer is NULL */
+#define LMRS_ERR_BAD_DTYPE -2      /* dtype not in {BF16, F32} */
+#define LMRS_ERR_BAD_SHAPE -3      /* batch < 0, vocab < 0, row_stride < vocab, or vocab > LMRS_MAX_VOCAB */
+#define LMRS_ERR_LAUNCH -4         /* the HIP launch failed (see hipGetLastError) */
+#define LMRS_ERR_ALIGNMENT -5      /* logits pointer not aligned to its element size */
+
+/* Per-row status codes written to status[r] (low byte) ... */
+#define LMRS_ROW_OK 0
+#define LMRS_ROW_EMPTY 1        /* vocab == 0: "cannot sample from empty logits" (strategies/greedy.rs:24-26) */
+#define LMRS_ROW_DISTRIBUTION 2 /* non-finite or non-positive weight sum (strategies/mod.rs:39-43) */
+#define LMRS_ROW_PARAM 3        /* a parameter fails its constructor's validation (repetition.rs:57-64,
+                                   presence.rs:61-71, temperature.rs:43-50, top_p.rs:26-31); top_k < 0 */
+#define LMRS_ROW_HISTORY 4      /* history longer than LMRS_MAX_HISTORY for this row */
+/* ... and flag bits above it. */
+#define LMRS_ROW_NEAR_BOUNDARY 0x100 /* the uniform lies within 1e-6 of a CDF boundary of the chosen
+                                        token, or the nucleus cumulative lies within 1e-6 of top_p at
+                                        the cut: the reference's f64 summation order may pick a
+                                        neighbouring token here */
+
+#define LMRS_MAX_VOCAB 262144  /* largest vocab accepted (2^18) */
+#define LMRS_MAX_HISTORY 4096  /* longest per-row history accepted */
+
+typedef struct lmrs_sample_args {
+  /* logits: device, `batch` rows of `row_stride` elements of `dtype`; only the
+   * first `vocab` elements of a row are read.  Never written. */
+  const void *logits;
+  int32_t dtype;
+  int32_t batch;
+  int64_t vocab;
+  int64_t row_stride;
+
+  /* Token history per row in CSR form (device): the ids of row r are
+   * hist_ids[hist_offsets[r] .. hist_offsets[r+1]).  Ids >= vocab are ignored
+   * (repetition.rs:93, presence.rs:113).  hist_offsets == NULL: no history. */
+  const int64_t *hist_offsets;
+  const uint32_t *hist_ids;
+
+  /* Per-row parameters (device arrays of length batch; NULL = the neutral
+   * value, which skips the processor exactly as the reference does). */
+  const float *repetition_penalty; /* finite, > 0; 1.0 = off (repetition.rs:82) */
+  const float *presence_penalty;   /* finite; 0 = off together with frequency (presence.rs:102) */
+  const float *frequency_penalty;  /* finite */
+  const double *temperature;       /* finite, > 0; 1.0 = off (temperature.rs:68) */
+  const int32_t *top_k;            /* >= 0; 0 = off, 1 = greedy */
+  const double *top_p;             /* in (0, 1]; 1.0 = off */
+  const double *uniforms;          /* in [0, 1): the draw's uniform (next_unit of the reference's
+                                      LCG, strategies/mod.rs:57-61, or any caller RNG).  Required
+                                      unless every row is greedy; NULL reads as 0. */
+
+  /* Outputs (device, length batch).  token_ids is required. */
+  uint32_t *token_ids; /* SampleOutput::token_id (sampler/output.rs:14-18) */
+  float *log_probs;    /* ln of the chosen token's post-filter probability; 0 for greedy */
+  float *logits_out;   /* processed logit of the chosen token */
+  int32_t *status;     /* per-row LMRS_ROW_* code | flags */
+} lmrs_sample_args;
+
+/* Samples one token per row (the fused replacement of Sampler::sample over a
+ * batch).  Asynchronous on `stream`.  Returns LMRS_OK or an LMRS_ERR_* code;
+ * per-row problems are reported in status[r] and never fail the call. */
+int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream);
+
+/* Applies the processor chain only (Repetition -> Presence/Frequency ->
+ * Temperature, each skipped per its own rule) and writes the processed rows,
+ * in the input dtype, to `out` ([batch, vocab] contiguous, device).  This is
+ * LogitsProcessor::process (crates/sampling/src/logits/processor.rs:21-24)
+ * for the three reference processors, batched.  Uses args' logits, dtype,
+ * batch, vocab, row_stride, history and the three penalty / temperature
+ * arrays; ignores the rest. */
+int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, void *stream);
+
+/* Library version string. */
+const char *lmrs_sampling_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LMRS_SAMPLING_H */

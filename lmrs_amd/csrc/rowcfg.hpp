@@ -1,0 +1,178 @@
+// rowcfg.hpp -- per-row parameters, history tables and the processor chain.
+//
+// The processor chain is the reference's Sampler::sample loop
+// (crates/sampling/src/sampler/sampler.rs:178-186) over the processors
+// Repetition -> Presence/Frequency -> Temperature, each with its own skip
+// rule, fused into one per-element function.  bf16 rows round after every
+// op exactly as the reference's chain of bf16 kernels does; f32 rows use the
+// same ops without rounding.
+#pragma once
+
+#include "../../include/lmrs_sampling.h"
+#include "common.hpp"
+
+namespace lmrs {
+
+constexpr int kHashCap = 2 * LMRS_MAX_HISTORY;  // open addressing, load <= 1/2
+constexpr int kHashBits = 13;
+static_assert((1 << kHashBits) == kHashCap, "hash size");
+constexpr int kBitmapWords = LMRS_MAX_VOCAB / 32;
+
+struct RowCfg {
+  int status;          // LMRS_ROW_OK or an error code decided before sampling
+  int rep_on, pres_on, temp_on, hist_on;
+  float pf, nf;        // repetition factors (bf16-rounded for bf16 rows)
+  float presence, frequency;
+  float scale;         // (float)(1.0 / T)
+  int64_t top_k;       // 0 = off
+  double top_p;        // >= 1.0 = off
+  double u;
+  int64_t h_begin, h_len;
+};
+
+// History tables in LDS: a membership bitmap over the vocab and a hash map
+// token -> multiplicity (the HashMap of presence.rs:107-110).
+struct HistoryTables {
+  uint32_t keys[kHashCap];   // token + 1, 0 = empty
+  uint32_t counts[kHashCap];
+  uint32_t bitmap[kBitmapWords];
+};
+
+__device__ __forceinline__ uint32_t hash_slot(uint32_t t) {
+  return (t * 2654435761u) >> (32 - kHashBits);
+}
+
+__device__ __forceinline__ uint32_t history_count(const HistoryTables &ht, uint32_t t) {
+  uint32_t s = hash_slot(t);
+  for (;;) {  // terminates: the table is at most half full
+    uint32_t k = ht.keys[s];
+    if (k == t + 1u) return ht.counts[s];
+    if (k == 0u) return 0u;
+    s = (s + 1u) & (kHashCap - 1);
+  }
+}
+
+__device__ __forceinline__ bool history_member(const HistoryTables &ht, uint32_t i) {
+  return (ht.bitmap[i >> 5] >> (i & 31u)) & 1u;
+}
+
+// Reads and validates row r's parameters (thread 0 only).  Validation
+// mirrors the constructors: RepetitionPenalty::new (repetition.rs:57-64),
+// FrequencyPresencePenalty::new (presence.rs:61-71), Temperature::new
+// (temperature.rs:43-50), TopP::new (top_p.rs:26-31); top_k < 0 invalid.
+__device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype) {
+  RowCfg c;
+  c.status = LMRS_ROW_OK;
+  float rep = a.repetition_penalty ? a.repetition_penalty[r] : 1.0f;
+  float pres = a.presence_penalty ? a.presence_penalty[r] : 0.0f;
+  float freq = a.frequency_penalty ? a.frequency_penalty[r] : 0.0f;
+  double t = a.temperature ? a.temperature[r] : 1.0;
+  int64_t k = a.top_k ? (int64_t)a.top_k[r] : 0;
+  double p = a.top_p ? a.top_p[r] : 1.0;
+  c.u = a.uniforms ? a.uniforms[r] : 0.0;
+  if (!(__builtin_isfinite(rep) && rep > 0.0f) || !__builtin_isfinite(pres) ||
+      !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < 0 ||
+      !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0))
+    c.status = LMRS_ROW_PARAM;
+  c.h_begin = 0;
+  c.h_len = 0;
+  if (a.hist_offsets) {
+    c.h_begin = a.hist_offsets[r];
+    c.h_len = a.hist_offsets[r + 1] - c.h_begin;
+    if (c.h_len < 0) c.status = LMRS_ROW_PARAM;
+    if (c.h_len > LMRS_MAX_HISTORY && c.status == LMRS_ROW_OK) c.status = LMRS_ROW_HISTORY;
+  }
+  const bool has_hist = c.h_len > 0;
+  c.rep_on = (rep != 1.0f) && has_hist;                        // repetition.rs:82-84
+  c.pres_on = has_hist && !(pres == 0.0f && freq == 0.0f);     // presence.rs:102-104
+  c.temp_on = (t != 1.0);                                      // temperature.rs:68-70
+  c.hist_on = c.rep_on || c.pres_on;
+  float inv = 1.0f / rep;                                      // repetition.rs:88 (IEEE division)
+  if (dtype == LMRS_DTYPE_BF16) {
+    c.pf = round_bf16_host(inv);                               // repetition.rs:104-105
+    c.nf = round_bf16_host(rep);
+  } else {
+    c.pf = inv;
+    c.nf = rep;
+  }
+  c.presence = pres;
+  c.frequency = freq;
+  c.scale = (float)(1.0 / t);                                  // temperature.rs:71
+  c.top_k = k;
+  c.top_p = p;
+  return c;
+}
+
+// Builds the history tables for the row (all threads; ends with a barrier).
+__device__ inline void build_history(HistoryTables &ht, const lmrs_sample_args &a,
+                                     const RowCfg &c, int64_t vocab) {
+  for (int i = threadIdx.x; i < kHashCap; i += kThreads) {
+    ht.keys[i] = 0u;
+    ht.counts[i] = 0u;
+  }
+  const int words = (int)((vocab + 31) >> 5);
+  for (int i = threadIdx.x; i < words; i += kThreads) ht.bitmap[i] = 0u;
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < c.h_len; j += kThreads) {
+    uint32_t t = a.hist_ids[c.h_begin + j];
+    if ((int64_t)t >= vocab) continue;  // ids outside the vocab are ignored
+    atomicOr(&ht.bitmap[t >> 5], 1u << (t & 31u));
+    uint32_t s = hash_slot(t);
+    for (;;) {
+      uint32_t prev = atomicCAS(&ht.keys[s], 0u, t + 1u);
+      if (prev == 0u || prev == t + 1u) {
+        atomicAdd(&ht.counts[s], 1u);
+        break;
+      }
+      s = (s + 1u) & (kHashCap - 1);
+    }
+  }
+  __syncthreads();
+}
+
+// The processor chain on one bf16 element (16-bit pattern in, out).
+// Repetition (repetition.rs:113-116): mul by the positive / negative factor
+// tensors (1.0 off the history), greater_equal(x, 0), where.  Presence
+// (presence.rs:114, 123-129): sub of bf16(presence + frequency * count).
+// Temperature (temperature.rs:71, tensor_ffi.cu:55-56): fma(x, s, 0).
+__device__ __forceinline__ uint32_t process_bf16(uint32_t x, uint32_t idx, const RowCfg &c,
+                                                 const HistoryTables &ht) {
+  if (!(c.hist_on | c.temp_on)) return x;
+  float v = bf16_to_f32(x);
+  bool member = c.hist_on ? history_member(ht, idx) : false;
+  if (c.rep_on) {
+    float fp = member ? c.pf : 1.0f, fn = member ? c.nf : 1.0f;
+    float pos = round_bf16_dev(v * fp), neg = round_bf16_dev(v * fn);
+    v = (v >= 0.0f) ? pos : neg;
+  }
+  if (c.pres_on) {
+    float pen = 0.0f;
+    if (member) {
+      float cnt = (float)history_count(ht, idx);
+      pen = round_bf16_host(c.presence + c.frequency * cnt);
+    }
+    v = round_bf16_dev(v - pen);
+  }
+  if (c.temp_on) v = round_bf16_dev(__builtin_fmaf(v, c.scale, 0.0f));
+  return __float_as_uint(v) >> 16;
+}
+
+// The same chain on one f32 element, without bf16 rounding.
+__device__ __forceinline__ float process_f32(float v, uint32_t idx, const RowCfg &c,
+                                             const HistoryTables &ht) {
+  if (!(c.hist_on | c.temp_on)) return v;
+  bool member = c.hist_on ? history_member(ht, idx) : false;
+  if (c.rep_on) {
+    float fp = member ? c.pf : 1.0f, fn = member ? c.nf : 1.0f;
+    v = (v >= 0.0f) ? v * fp : v * fn;
+  }
+  if (c.pres_on) {
+    float pen = 0.0f;
+    if (member) pen = c.presence + c.frequency * (float)history_count(ht, idx);
+    v = v - pen;
+  }
+  if (c.temp_on) v = __builtin_fmaf(v, c.scale, 0.0f);
+  return v;
+}
+
+}  // namespace lmrs

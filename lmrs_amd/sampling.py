@@ -1,0 +1,355 @@
+"""Python binding of the HIP sampler's C-ABI (include/lmrs_sampling.h).
+
+This is the host-side mirror of lmrs's ``crates/sampling`` API for Python
+callers: ``Sampler`` / ``SamplerConfig`` / strategies / processors with the
+reference's names and validation, plus ``sample_batch`` (per-row params in,
+one token id per row out).  PyTorch only supplies device memory and the
+stream; all sampling work runs in ``liblmrs_sampling.so``.  There is no CPU
+fallback: importing this module without the built library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblmrs_sampling.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "lmrs_sampling.h")
+
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+
+LMRS_OK = 0
+ERR_NULL_ARGUMENT, ERR_BAD_DTYPE, ERR_BAD_SHAPE, ERR_LAUNCH, ERR_ALIGNMENT = -1, -2, -3, -4, -5
+ROW_OK, ROW_EMPTY, ROW_DISTRIBUTION, ROW_PARAM, ROW_HISTORY = 0, 1, 2, 3, 4
+ROW_NEAR_BOUNDARY = 0x100
+MAX_VOCAB = 262144
+MAX_HISTORY = 4096
+
+
+class SampleArgs(ctypes.Structure):
+    """Mirror of ``lmrs_sample_args``."""
+
+    _fields_ = [
+        ("logits", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("vocab", ctypes.c_int64),
+        ("row_stride", ctypes.c_int64),
+        ("hist_offsets", ctypes.c_void_p),
+        ("hist_ids", ctypes.c_void_p),
+        ("repetition_penalty", ctypes.c_void_p),
+        ("presence_penalty", ctypes.c_void_p),
+        ("frequency_penalty", ctypes.c_void_p),
+        ("temperature", ctypes.c_void_p),
+        ("top_k", ctypes.c_void_p),
+        ("top_p", ctypes.c_void_p),
+        ("uniforms", ctypes.c_void_p),
+        ("token_ids", ctypes.c_void_p),
+        ("log_probs", ctypes.c_void_p),
+        ("logits_out", ctypes.c_void_p),
+        ("status", ctypes.c_void_p),
+    ]
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """The loaded HIP library (raises LibraryMissing when it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(f"{LIB_PATH} is not built: run `python -m lmrs_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.lmrs_sample_fwd.argtypes = [ctypes.POINTER(SampleArgs), ctypes.c_void_p]
+        L.lmrs_sample_fwd.restype = ctypes.c_int
+        L.lmrs_process_logits_fwd.argtypes = [ctypes.POINTER(SampleArgs), ctypes.c_void_p, ctypes.c_void_p]
+        L.lmrs_process_logits_fwd.restype = ctypes.c_int
+        L.lmrs_sampling_version.argtypes = []
+        L.lmrs_sampling_version.restype = ctypes.c_char_p
+        _lib = L
+    return _lib
+
+
+class SamplingError(RuntimeError):
+    """Mirror of SamplingError (crates/sampling/src/error.rs:20-39)."""
+
+
+# ---------------------------------------------------------------------------
+# device plumbing (torch tensors -> raw pointers)
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch  # noqa: WPS433 (imported lazily: only device plumbing)
+
+    return torch
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _dev_array(values, dtype, device):
+    torch = _torch()
+    if values is None:
+        return None
+    if isinstance(values, torch.Tensor):
+        return values.to(device=device, dtype=dtype).contiguous()
+    return torch.tensor(values, dtype=dtype, device=device)
+
+
+def history_csr(histories: Sequence[Sequence[int]], device):
+    """CSR (offsets int64 [B+1], ids uint32 as int32 storage) on `device`."""
+    torch = _torch()
+    offs = [0]
+    flat: list[int] = []
+    for h in histories:
+        flat.extend(int(t) for t in h)
+        offs.append(len(flat))
+    off_t = torch.tensor(offs, dtype=torch.int64, device=device)
+    ids = torch.tensor([t if t < 2**31 else t - 2**32 for t in flat] or [0], dtype=torch.int32, device=device)
+    return off_t, ids
+
+
+def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
+                 presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
+                 top_p=None, uniforms=None, stream=None, out=None):
+    """Samples one token per row of a [B, V] bf16/f32 CUDA tensor.
+
+    Per-row parameters are tensors or sequences of length B (None = neutral).
+    Returns dict(token_ids uint32-as-int32, log_probs f32, logits f32, status i32),
+    all on the logits' device; the call is asynchronous on `stream`.
+    """
+    torch = _torch()
+    if logits.dim() != 2:
+        raise ValueError("logits must be [batch, vocab]")
+    if logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    dev = logits.device
+    B, V = logits.shape
+    dt = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.float16: DTYPE_F16}.get(logits.dtype)
+    if dt is None:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    rp = _dev_array(repetition_penalty, torch.float32, dev)
+    pp = _dev_array(presence_penalty, torch.float32, dev)
+    fp = _dev_array(frequency_penalty, torch.float32, dev)
+    tt = _dev_array(temperature, torch.float64, dev)
+    tk = _dev_array(top_k, torch.int32, dev)
+    tp = _dev_array(top_p, torch.float64, dev)
+    uu = _dev_array(uniforms, torch.float64, dev)
+    if out is None:
+        out = {
+            "token_ids": torch.empty(B, dtype=torch.int32, device=dev),
+            "log_probs": torch.empty(B, dtype=torch.float32, device=dev),
+            "logits": torch.empty(B, dtype=torch.float32, device=dev),
+            "status": torch.empty(B, dtype=torch.int32, device=dev),
+        }
+    args = SampleArgs(
+        _ptr(logits), dt, B, V, logits.stride(0) if B > 0 else V,
+        _ptr(hist_offsets), _ptr(hist_ids), _ptr(rp), _ptr(pp), _ptr(fp), _ptr(tt), _ptr(tk), _ptr(tp), _ptr(uu),
+        _ptr(out["token_ids"]), _ptr(out["log_probs"]), _ptr(out["logits"]), _ptr(out["status"]),
+    )
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    rc = lib().lmrs_sample_fwd(ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
+    if rc != LMRS_OK:
+        raise SamplingError(f"lmrs_sample_fwd failed with code {rc}")
+    # keep argument tensors alive until the stream has consumed them
+    out["_keep"] = (rp, pp, fp, tt, tk, tp, uu, hist_offsets, hist_ids)
+    return out
+
+
+def process_logits(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
+                   presence_penalty=None, frequency_penalty=None, temperature=None, stream=None):
+    """The processor chain only (LogitsProcessor::process, batched); returns [B, V] in the input dtype."""
+    torch = _torch()
+    dev = logits.device
+    B, V = logits.shape
+    dt = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32}.get(logits.dtype)
+    if dt is None:
+        raise ValueError(f"unsupported logits dtype {logits.dtype}")
+    rp = _dev_array(repetition_penalty, torch.float32, dev)
+    pp = _dev_array(presence_penalty, torch.float32, dev)
+    fp = _dev_array(frequency_penalty, torch.float32, dev)
+    tt = _dev_array(temperature, torch.float64, dev)
+    status = torch.empty(B, dtype=torch.int32, device=dev)
+    out = torch.empty((B, V), dtype=logits.dtype, device=dev)
+    args = SampleArgs(_ptr(logits), dt, B, V, logits.stride(0) if B > 0 else V, _ptr(hist_offsets), _ptr(hist_ids),
+                      _ptr(rp), _ptr(pp), _ptr(fp), _ptr(tt), None, None, None, None, None, None, _ptr(status))
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    rc = lib().lmrs_process_logits_fwd(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()),
+                                       ctypes.c_void_p(s.cuda_stream))
+    if rc != LMRS_OK:
+        raise SamplingError(f"lmrs_process_logits_fwd failed with code {rc}")
+    torch.cuda.current_stream(dev).synchronize() if stream is None else None
+    return out, status
+
+
+# ---------------------------------------------------------------------------
+# mirror of the reference's single-row API (crates/sampling)
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class SampleOutput:
+    """SampleOutput (crates/sampling/src/sampler/output.rs:14-44)."""
+
+    token_id: int
+    log_prob: float
+    logit: float
+
+
+class SamplingStrategy:
+    """SamplingStrategy (strategies/mod.rs:16-19): maps onto kernel parameters."""
+
+    top_k = 0
+    top_p = 1.0
+    stochastic = True
+
+
+class Greedy(SamplingStrategy):
+    """Greedy (strategies/greedy.rs:19-29)."""
+
+    top_k = 1
+    stochastic = False
+
+
+class BeamSearch(SamplingStrategy):
+    """BeamSearch (strategies/beam.rs:23-50): the first sorted candidate."""
+
+    top_k = 1
+    stochastic = False
+
+    def __init__(self, width: int):
+        if width == 0:
+            raise SamplingError("beam width must be greater than zero")
+        self.width = width
+
+
+class TopK(SamplingStrategy):
+    """TopK (strategies/top_k.rs:19-45)."""
+
+    def __init__(self, k: int):
+        if k <= 0:
+            raise SamplingError("top_k must be greater than zero")
+        self.k = k
+        self.top_k = k
+
+
+class TopP(SamplingStrategy):
+    """TopP (strategies/top_p.rs:19-61)."""
+
+    def __init__(self, p: float):
+        if not math.isfinite(p) or p <= 0.0 or p > 1.0:
+            raise SamplingError("top_p must be in (0, 1]")
+        self.p = p
+        self.top_p = p
+
+
+class Temperature:
+    """Temperature (logits/temperature.rs:24-72)."""
+
+    def __init__(self, value: float):
+        if not math.isfinite(value) or value <= 0.0:
+            raise SamplingError("temperature must be finite and greater than zero")
+        self.value = float(value)
+
+
+class RepetitionPenalty:
+    """RepetitionPenalty (logits/repetition.rs:38-117)."""
+
+    def __init__(self, penalty: float):
+        if not math.isfinite(penalty) or penalty <= 0.0:
+            raise SamplingError("repetition penalty must be finite and greater than zero")
+        self.penalty = float(penalty)
+
+
+class FrequencyPresencePenalty:
+    """FrequencyPresencePenalty (logits/presence.rs:41-130)."""
+
+    def __init__(self, presence: float, frequency: float):
+        if not math.isfinite(presence) or not math.isfinite(frequency):
+            raise SamplingError("presence and frequency penalties must be finite")
+        self.presence = float(presence)
+        self.frequency = float(frequency)
+
+
+def next_unit(state: int) -> tuple[float, int]:
+    """The reference's LCG draw (strategies/mod.rs:57-61): returns (u, new_state)."""
+    state = (state * 6364136223846793005 + 1) & 0xFFFFFFFFFFFFFFFF
+    return ((state >> 11) & ((1 << 52) - 1)) / float(1 << 52), state
+
+
+class SamplerConfig:
+    """SamplerConfig (sampler/sampler.rs:21-72): strategy + LCG seed (default 1, min 1)."""
+
+    def __init__(self, strategy: Optional[SamplingStrategy] = None):
+        self.strategy = strategy if strategy is not None else Greedy()
+        self.seed = 1
+
+    def with_seed(self, seed: int) -> "SamplerConfig":
+        self.seed = max(int(seed), 1)
+        return self
+
+
+class Sampler:
+    """Sampler (sampler/sampler.rs:106-201) over the fused HIP kernel.
+
+    Processors are applied in push order as the reference does, but only the
+    reference's three processor kinds are supported, and each kind at most
+    once, in the order Repetition -> Presence/Frequency -> Temperature (the
+    fused kernel's fixed order); other orders raise SamplingError.
+    """
+
+    _ORDER = (RepetitionPenalty, FrequencyPresencePenalty, Temperature)
+
+    def __init__(self, config: Optional[SamplerConfig] = None):
+        config = config or SamplerConfig()
+        self.strategy = config.strategy
+        self.rng = config.seed
+        self.processors: list = []
+
+    def push_processor(self, processor) -> None:
+        kinds = [type(p) for p in self.processors] + [type(processor)]
+        pos = [self._ORDER.index(k) if k in self._ORDER else -1 for k in kinds]
+        if -1 in pos or pos != sorted(set(pos)):
+            raise SamplingError("the fused sampler applies Repetition, Presence/Frequency, Temperature in that order")
+        self.processors.append(processor)
+
+    def processor_count(self) -> int:
+        return len(self.processors)
+
+    def sample(self, logits, history: Sequence[int] = ()) -> SampleOutput:
+        """One row (any shape, flattened), like Sampler::sample."""
+        torch = _torch()
+        row = logits.reshape(1, -1)
+        kw = {}
+        for p in self.processors:
+            if isinstance(p, RepetitionPenalty):
+                kw["repetition_penalty"] = [p.penalty]
+            elif isinstance(p, FrequencyPresencePenalty):
+                kw["presence_penalty"] = [p.presence]
+                kw["frequency_penalty"] = [p.frequency]
+            elif isinstance(p, Temperature):
+                kw["temperature"] = [p.value]
+        off, ids = history_csr([list(history)], row.device)
+        u, saved = 0.0, self.rng
+        if self.strategy.stochastic:
+            u, self.rng = next_unit(self.rng)
+        res = sample_batch(row, hist_offsets=off, hist_ids=ids, top_k=[self.strategy.top_k],
+                           top_p=[self.strategy.top_p], uniforms=[u], **kw)
+        torch.cuda.current_stream(row.device).synchronize()
+        st = int(res["status"][0].item()) & 0xFF
+        if st != ROW_OK:
+            self.rng = saved  # the reference draws only after validation (strategies/mod.rs:39-44)
+            raise SamplingError({ROW_EMPTY: "cannot sample from empty logits",
+                                 ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
+                                 ROW_PARAM: "invalid sampling parameter",
+                                 ROW_HISTORY: "history too long"}.get(st, f"status {st}"))
+        return SampleOutput(int(res["token_ids"][0].item()) & 0xFFFFFFFF, float(res["log_probs"][0].item()),
+                            float(res["logits"][0].item()))

@@ -1,0 +1,86 @@
+"""Shared helpers for the GPU parity tests: run a workload through the HIP
+library (via its C-ABI) and through the CPU oracle, and compare."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+
+BOUNDARY = 1e-6      # |u - CDF boundary| or |nucleus cumulative - p| below this is ambiguous
+PROB_RTOL = 1e-5     # post-filter probability tolerance (relative)
+
+
+def to_device(w, device="cuda"):
+    import torch
+
+    if w.logits.dtype == np.uint16:
+        logits = torch.from_numpy(w.logits.view(np.int16)).view(torch.bfloat16).to(device)
+    else:
+        logits = torch.from_numpy(w.logits).to(device)
+    off = ids = None
+    if w.hist_offsets is not None:
+        off = torch.from_numpy(w.hist_offsets.astype(np.int64)).to(device)
+        ids = torch.from_numpy(w.hist_ids.astype(np.uint32).view(np.int32)).to(device)
+    return logits, off, ids
+
+
+def run_gpu(w, logits=None, off=None, ids=None):
+    import torch
+
+    from lmrs_amd import sampling as S
+
+    if logits is None:
+        logits, off, ids = to_device(w)
+    res = S.sample_batch(logits, hist_offsets=off, hist_ids=ids, repetition_penalty=w.repetition_penalty,
+                         presence_penalty=w.presence_penalty, frequency_penalty=w.frequency_penalty,
+                         temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, uniforms=w.uniforms)
+    torch.cuda.synchronize()
+    return {
+        "token_id": res["token_ids"].cpu().numpy().view(np.uint32),
+        "log_prob": res["log_probs"].cpu().numpy(),
+        "logit": res["logits"].cpu().numpy(),
+        "status": res["status"].cpu().numpy(),
+    }
+
+
+def run_oracle(w, threads=None):
+    import oracle as O
+
+    params = [O.make_params(float(w.repetition_penalty[r]), float(w.presence_penalty[r]),
+                            float(w.frequency_penalty[r]), float(w.temperature[r]), int(w.top_k[r]),
+                            float(w.top_p[r])) for r in range(w.batch)]
+    threads = threads or min(16, os.cpu_count() or 1)
+    return O.sample_batch(w.logits, w.hist_offsets, w.hist_ids, params, w.uniforms, n_threads=threads)
+
+
+def compare(gpu, ref):
+    """Returns a report dict; asserts nothing."""
+    st_gpu = gpu["status"] & 0xFF
+    ok = ref["status"] == 0
+    boundary = ok & ((ref["cdf_margin"] < BOUNDARY) | (ref["top_p_margin"] < BOUNDARY))
+    same = gpu["token_id"] == ref["token_id"]
+    status_mismatch = int(np.sum(st_gpu != ref["status"]))
+    mism = ok & ~same & ~boundary
+    both = ok & same
+    prob_gpu = np.exp(gpu["log_prob"].astype(np.float64))
+    rel = np.abs(prob_gpu - ref["prob"]) / np.maximum(ref["prob"], 1e-300)
+    rel = np.where(both, rel, 0.0)
+    logit_bad = int(np.sum(both & (gpu["logit"].view(np.uint32) != ref["logit"].view(np.uint32))))
+    return {
+        "rows": int(len(ok)),
+        "status_mismatch": status_mismatch,
+        "token_mismatch": int(np.sum(mism)),
+        "boundary_rows": int(np.sum(boundary)),
+        "boundary_mismatch": int(np.sum(boundary & ~same)),
+        "gpu_flagged": int(np.sum((gpu["status"] & 0x100) != 0)),
+        "max_prob_rel_err": float(np.max(rel)) if len(rel) else 0.0,
+        "logit_mismatch": logit_bad,
+        "mismatch_rows": np.nonzero(mism)[0][:10].tolist(),
+    }
+
+
+def assert_parity(rep, name=""):
+    assert rep["status_mismatch"] == 0, (name, rep)
+    assert rep["token_mismatch"] == 0, (name, rep)
+    assert rep["logit_mismatch"] == 0, (name, rep)
+    assert rep["max_prob_rel_err"] < PROB_RTOL, (name, rep)

@@ -1,0 +1,324 @@
+"""GPU parity tests: the HIP sampler (through its C-ABI) against the CPU oracle.
+
+Bar: token ids identical except rows where the oracle's uniform lies within
+1e-6 of a CDF boundary (or the nucleus cumulative within 1e-6 of top_p),
+which are counted; processed logit of the chosen token bit-identical;
+post-filter probability exp(log_prob) within 1e-5 relative.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import assert_parity, compare, run_gpu, run_oracle, to_device
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _require_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    _require_gpu()
+    from lmrs_amd import sampling as S
+
+    S.lib()  # fail loudly if the HIP library is missing
+
+
+def _wl():
+    from lmrs_amd import workloads as W
+
+    return W
+
+
+def _report(name, rep):
+    print(f"[parity] {name}: {rep}", flush=True)
+
+
+# ---------------------------------------------------------------------------
+# the five configurations (full vocab; batch trimmed where noted)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg,rows", [("C1", None), ("C2", None), ("C3", 64), ("C4", 128), ("C5", 24)])
+def test_config_parity(cfg, rows):
+    W = _wl()
+    kw = {"batch": rows} if rows else {}
+    if cfg == "C1":
+        kw = {"batch": 4}
+    w = W.CONFIGS[cfg](**kw)
+    print(f"[case] {cfg} B={w.batch} V={w.vocab} {w.dtype}", flush=True)
+    rep = compare(run_gpu(w), run_oracle(w))
+    _report(cfg, rep)
+    assert_parity(rep, cfg)
+
+
+def test_c1_greedy_check():
+    W = _wl()
+    w = W.c1(batch=2)
+    w.top_k[:] = 1
+    rep = compare(run_gpu(w), run_oracle(w))
+    assert_parity(rep, "C1-greedy")
+
+
+def test_c4_contiguous_halves():
+    W = _wl()
+    w = W.c4(batch=64, layout="halves")
+    rep = compare(run_gpu(w), run_oracle(w))
+    assert_parity(rep, "C4-halves")
+
+
+# ---------------------------------------------------------------------------
+# processors: exhaustive over all 65536 bf16 patterns
+# ---------------------------------------------------------------------------
+
+def test_processors_exhaustive_bf16():
+    import oracle as O
+
+    from lmrs_amd import sampling as S
+
+    V = 65536
+    allb = np.arange(V, dtype=np.uint32).astype(np.uint16)
+    configs = [(1.1, 0.5, 0.3, 0.7), (2.0, 0.0, 0.0, 1.0), (0.7, -1.0, 0.125, 1.5), (1.0, 0.5, 0.25, 1e-3),
+               (1.05, 0.0, 0.7, 3.0)]
+    B = len(configs)
+    x = np.tile(allb, (B, 1))
+    hist = np.concatenate([np.arange(0, V, 3), np.arange(0, V, 7), [V + 5]]).astype(np.uint32)
+    off = np.arange(0, (B + 1) * len(hist), len(hist), dtype=np.int64)
+    ids = np.tile(hist, B)
+    logits = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
+    out, status = S.process_logits(logits, hist_offsets=torch.from_numpy(off).cuda(),
+                                   hist_ids=torch.from_numpy(ids.view(np.int32)).cuda(),
+                                   repetition_penalty=[c[0] for c in configs],
+                                   presence_penalty=[c[1] for c in configs],
+                                   frequency_penalty=[c[2] for c in configs],
+                                   temperature=[c[3] for c in configs])
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    for r, (rep, pres, freq, t) in enumerate(configs):
+        want = allb.copy()
+        want = O.repetition(want, rep, hist)[1]
+        want = O.presence(want, pres, freq, hist)[1]
+        want = O.temperature(want, t)[1]
+        bad = np.nonzero(got[r] != want)[0]
+        assert len(bad) == 0, (configs[r], bad[:8], got[r][bad[:8]], want[bad[:8]])
+    assert np.all(status.cpu().numpy() == 0)
+
+
+def test_processors_f32():
+    import oracle as O
+
+    from lmrs_amd import sampling as S
+
+    rng = np.random.default_rng(11)
+    V = 50000
+    x = (rng.standard_normal((3, V)) * 4).astype(np.float32)
+    hist = rng.integers(0, V, 700).astype(np.uint32)
+    off = np.array([0, 700, 1400, 2100], np.int64)
+    ids = np.tile(hist, 3)
+    params = [(1.05, 0.0, 0.0, 1.0), (1.3, 0.4, 0.2, 0.8), (0.9, -0.5, 0.1, 2.5)]
+    out, _ = S.process_logits(torch.from_numpy(x).cuda(), hist_offsets=torch.from_numpy(off).cuda(),
+                              hist_ids=torch.from_numpy(ids.view(np.int32)).cuda(),
+                              repetition_penalty=[p[0] for p in params], presence_penalty=[p[1] for p in params],
+                              frequency_penalty=[p[2] for p in params], temperature=[p[3] for p in params])
+    got = out.cpu().numpy()
+    for r, (rep, pres, freq, t) in enumerate(params):
+        want = O.temperature(O.presence(O.repetition(x[r], rep, hist)[1], pres, freq, hist)[1], t)[1]
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# edge cases
+# ---------------------------------------------------------------------------
+
+def _mk(logits, **kw):
+    """A Workload from explicit rows (numpy float32 or uint16 bf16 bits)."""
+    W = _wl()
+    B = logits.shape[0]
+    f = lambda name, val, dt: np.asarray(kw.get(name, [val] * B), dtype=dt)  # noqa: E731
+    hist = kw.get("history")
+    off = ids = None
+    if hist is not None:
+        off = np.concatenate([[0], np.cumsum([len(h) for h in hist])]).astype(np.int64)
+        ids = np.concatenate([np.asarray(h, np.uint32) for h in hist]).astype(np.uint32)
+    return W.Workload("edge", logits, f("rep", 1.0, np.float32), f("pres", 0.0, np.float32),
+                      f("freq", 0.0, np.float32), f("t", 1.0, np.float64), f("k", 0, np.int32),
+                      f("p", 1.0, np.float64), f("u", 0.5, np.float64), off, ids)
+
+
+def test_ties_and_small_rows():
+    W = _wl()
+    rows = []
+    rng = np.random.default_rng(12)
+    V = 37
+    for _ in range(48):
+        rows.append(rng.choice(np.array([0.0, 1.0, 1.0, 2.0, -0.0, 0.5], np.float32), size=V))
+    x = np.stack(rows)
+    B = len(rows)
+    k = rng.choice(np.array([0, 1, 2, 3, 5, 36, 37, 100], np.int32), B)
+    p = rng.choice(np.array([1.0, 0.3, 0.5, 0.9, 0.999]), B)
+    u = np.concatenate([[0.0, 0.9999999999], rng.random(B - 2)])
+    for dt in ("f32", "bf16"):
+        xx = x if dt == "f32" else W.f32_to_bf16_bits(x)
+        w = _mk(xx, k=k, p=p, u=u)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"ties-{dt}", rep)
+        assert_parity(rep, dt)
+
+
+def test_all_equal_row_and_large_tie_groups():
+    W = _wl()
+    V = 30000
+    B = 8
+    x = np.zeros((B, V), np.float32)
+    x[1::2, ::3] = 1.0  # many tied maxima (10000) on odd rows
+    k = np.array([0, 0, 5000, 5000, 12000, 20000, 1, 1], np.int32)
+    p = np.array([1.0, 0.5, 1.0, 0.7, 0.95, 0.3, 1.0, 1.0])
+    u = np.linspace(0.05, 0.95, B)
+    for dt in ("f32", "bf16"):
+        xx = x if dt == "f32" else W.f32_to_bf16_bits(x)
+        w = _mk(xx, k=k, p=p, u=u)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"bigties-{dt}", rep)
+        assert_parity(rep, dt)
+
+
+def test_vocab_sizes_and_unaligned_rows():
+    import torch as T
+
+    W = _wl()
+    rng = np.random.default_rng(13)
+    for V in (1, 2, 3, 7, 8, 9, 1000, 4097, 33333):
+        x = (rng.standard_normal((6, V)) * 2).astype(np.float32)
+        k = np.array([0, 1, 2, 10, 0, 3], np.int32)
+        p = np.array([1.0, 1.0, 0.9, 0.5, 0.8, 1.0])
+        for dt in ("f32", "bf16"):
+            xx = x if dt == "f32" else W.f32_to_bf16_bits(x)
+            w = _mk(xx, k=k, p=p, u=rng.random(6))
+            # unaligned rows: a row stride of V + 1 elements, starting one element in
+            if xx.dtype == np.uint16:
+                big = T.zeros((6, V + 1), dtype=T.int16)
+                big[:, 1:] = T.from_numpy(xx.view(np.int16))
+                logits = big.view(T.bfloat16).cuda()[:, 1:]
+            else:
+                big = T.zeros((6, V + 1), dtype=T.float32)
+                big[:, 1:] = T.from_numpy(xx)
+                logits = big.cuda()[:, 1:]
+            ref = run_oracle(w)
+            rep = compare(run_gpu(w, logits=logits), ref)
+            assert_parity(rep, f"unaligned V={V} {dt}")
+            rep = compare(run_gpu(w), ref)
+            assert_parity(rep, f"aligned V={V} {dt}")
+
+
+def test_special_values_and_statuses():
+    from lmrs_amd import sampling as S
+
+    V = 16
+    x = np.zeros((8, V), np.float32)
+    x[0, 3] = np.nan                      # NaN row, sampled -> invalid distribution
+    x[1, 3] = np.nan                      # NaN row, greedy -> the NaN's index
+    x[2, 5] = np.inf                      # +inf -> invalid distribution
+    x[3, :] = -np.inf                     # all -inf -> invalid distribution
+    x[4, :] = -np.inf
+    x[4, 7] = 1.0                         # one finite token
+    x[5, :] = np.linspace(-3, 3, V)
+    x[6, :] = -0.0
+    x[6, 2] = 0.0                         # +0 sorts above -0
+    x[7, :] = np.linspace(0, 1, V)
+    k = np.array([0, 1, 0, 0, 0, 0, 1, 0], np.int32)
+    p = np.array([1.0, 1.0, 1.0, 1.0, 0.5, 1.0, 1.0, 1.0])
+    t = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 0.0, 1.0, 1.0])   # row 5: invalid temperature
+    w = _mk(x, k=k, p=p, t=t, u=np.full(8, 0.7))
+    g, r = run_gpu(w), run_oracle(w)
+    assert list(g["status"] & 0xFF) == list(r["status"]), (g["status"], r["status"])
+    assert list(r["status"]) == [2, 0, 2, 2, 0, 3, 0, 0]
+    ok = r["status"] == 0
+    assert np.array_equal(g["token_id"][ok], r["token_id"][ok])
+    # empty vocab
+    w0 = _mk(np.zeros((2, 0), np.float32))
+    g0 = run_gpu(w0)
+    assert list(g0["status"]) == [S.ROW_EMPTY] * 2
+
+
+def test_history_limits_and_out_of_range_ids():
+    from lmrs_amd import sampling as S
+
+    W = _wl()
+    rng = np.random.default_rng(14)
+    V = 5000
+    x = W.f32_to_bf16_bits((rng.standard_normal((3, V)) * 2).astype(np.float32))
+    hist = [list(rng.integers(0, V, 100)) + [V, V + 1, 2**32 - 1],   # out-of-range ids ignored
+            list(rng.integers(0, V, S.MAX_HISTORY)),                 # at the limit
+            list(rng.integers(0, V, S.MAX_HISTORY + 1))]             # over the limit
+    w = _mk(x, history=hist, rep=[1.3] * 3, pres=[0.4] * 3, freq=[0.2] * 3, t=[0.9] * 3, k=[40] * 3,
+            p=[0.9] * 3, u=[0.3, 0.6, 0.9])
+    g = run_gpu(w)
+    assert (g["status"][2] & 0xFF) == S.ROW_HISTORY
+    r = run_oracle(w.rows([0, 1]))
+    sub = {k: v[:2] for k, v in g.items()}
+    assert_parity(compare(sub, r), "history")
+
+
+def test_uniform_extremes():
+    W = _wl()
+    rng = np.random.default_rng(15)
+    V = 2000
+    x = W.f32_to_bf16_bits((rng.standard_normal((6, V)) * 2).astype(np.float32))
+    u = np.array([0.0, 2.0**-52, 0.5, 1 - 2.0**-52, 1 - 1e-9, 0.25])
+    k = np.array([0, 0, 0, 0, 50, 50], np.int32)
+    p = np.array([1.0, 0.9, 1.0, 1.0, 0.9, 1.0])
+    w = _mk(x, k=k, p=p, u=u)
+    rep = compare(run_gpu(w), run_oracle(w))
+    assert_parity(rep, "uniforms")
+
+
+# ---------------------------------------------------------------------------
+# the Python mirror of the reference API
+# ---------------------------------------------------------------------------
+
+def test_sampler_api_matches_reference_strategies():
+    import oracle as O
+
+    from lmrs_amd import sampling as S
+
+    x = torch.tensor([0.0, 10.0, 9.0], dtype=torch.bfloat16).cuda()
+    s = S.Sampler(S.SamplerConfig(S.TopK(2)).with_seed(42))
+    rng = 42
+    for _ in range(6):
+        got = s.sample(x, [])
+        st, want, rng = O.top_k(np.array([0.0, 10.0, 9.0], np.float32), 2, rng)
+        assert got.token_id == want[0]
+        assert math.isclose(got.log_prob, want[1], rel_tol=1e-5)
+    assert s.rng == rng
+    g = S.Sampler()  # default: Greedy, seed 1
+    assert g.sample(torch.tensor([0.0, 3.0, 1.0], dtype=torch.bfloat16).cuda()).token_id == 1
+    assert g.sample(torch.tensor([1.0, 5.0, 2.0], dtype=torch.bfloat16).cuda()).token_id == 1
+    # processors through the mirror
+    sp = S.Sampler(S.SamplerConfig(S.TopP(0.9)).with_seed(9))
+    sp.push_processor(S.RepetitionPenalty(2.0))
+    sp.push_processor(S.Temperature(0.5))
+    out = sp.sample(torch.tensor([2.0, -2.0, 1.0, 1.5], dtype=torch.bfloat16).cuda(), [0, 1])
+    row = np.array([O.bf16_host(v) for v in [2.0, -2.0, 1.0, 1.5]], np.uint16)
+    u, _ = O.next_unit(9)
+    st, want, _, _ = O.sample_row(row, [0, 1], O.make_params(repetition_penalty=2.0, temperature=0.5, top_p=0.9), u)
+    assert out.token_id == want[0]
+    with pytest.raises(S.SamplingError):
+        S.Sampler().sample(torch.zeros(0, dtype=torch.bfloat16).cuda())
+
+
+def test_engine_one_hot_decode_loop():
+    from lmrs_amd import sampling as S
+
+    V = 8
+    s = S.Sampler()
+    got = []
+    for tok in (3, 4, 5):  # ScriptModel of crates/engine/tests/prefill_decode.rs:37-84
+        row = torch.zeros(1, 1, V, dtype=torch.bfloat16)
+        row[0, 0, tok] = 100.0
+        got.append(s.sample(row.cuda(), got).token_id)
+    assert got == [3, 4, 5]
