@@ -130,10 +130,10 @@ def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty
     torch = _torch()
     if logits.dim() != 2:
         raise ValueError("logits must be [batch, vocab]")
-    if logits.stride(1) != 1:
+    B, V = logits.shape
+    if logits.stride(1) != 1 and V > 1:
         raise ValueError("logits rows must be contiguous")
     dev = logits.device
-    B, V = logits.shape
     dt = {torch.bfloat16: DTYPE_BF16, torch.float32: DTYPE_F32, torch.float16: DTYPE_F16}.get(logits.dtype)
     if dt is None:
         raise ValueError(f"unsupported logits dtype {logits.dtype}")

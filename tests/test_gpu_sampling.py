@@ -85,28 +85,33 @@ def test_processors_exhaustive_bf16():
     allb = np.arange(V, dtype=np.uint32).astype(np.uint16)
     configs = [(1.1, 0.5, 0.3, 0.7), (2.0, 0.0, 0.0, 1.0), (0.7, -1.0, 0.125, 1.5), (1.0, 0.5, 0.25, 1e-3),
                (1.05, 0.0, 0.7, 3.0)]
-    B = len(configs)
+    # each config runs on 32 rows whose histories (<= LMRS_MAX_HISTORY ids each)
+    # together mark every pattern once, twice (counts 2) or not at all
+    reps = 32
+    rows = [(c, o) for c in configs for o in range(reps)]
+    B = len(rows)
     x = np.tile(allb, (B, 1))
-    hist = np.concatenate([np.arange(0, V, 3), np.arange(0, V, 7), [V + 5]]).astype(np.uint32)
-    off = np.arange(0, (B + 1) * len(hist), len(hist), dtype=np.int64)
-    ids = np.tile(hist, B)
+    hists = [np.concatenate([np.arange(o, V, 2 * reps), np.arange(o, V, 4 * reps), [V + 5]]).astype(np.uint32)
+             for _, o in rows]
+    off = np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64)
+    ids = np.concatenate(hists)
     logits = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).cuda()
     out, status = S.process_logits(logits, hist_offsets=torch.from_numpy(off).cuda(),
                                    hist_ids=torch.from_numpy(ids.view(np.int32)).cuda(),
-                                   repetition_penalty=[c[0] for c in configs],
-                                   presence_penalty=[c[1] for c in configs],
-                                   frequency_penalty=[c[2] for c in configs],
-                                   temperature=[c[3] for c in configs])
+                                   repetition_penalty=[c[0] for c, _ in rows],
+                                   presence_penalty=[c[1] for c, _ in rows],
+                                   frequency_penalty=[c[2] for c, _ in rows],
+                                   temperature=[c[3] for c, _ in rows])
     torch.cuda.synchronize()
+    assert np.all(status.cpu().numpy() == 0)
     got = out.view(torch.int16).cpu().numpy().view(np.uint16)
-    for r, (rep, pres, freq, t) in enumerate(configs):
+    for r, ((rep, pres, freq, t), _) in enumerate(rows):
         want = allb.copy()
-        want = O.repetition(want, rep, hist)[1]
-        want = O.presence(want, pres, freq, hist)[1]
+        want = O.repetition(want, rep, hists[r])[1]
+        want = O.presence(want, pres, freq, hists[r])[1]
         want = O.temperature(want, t)[1]
         bad = np.nonzero(got[r] != want)[0]
-        assert len(bad) == 0, (configs[r], bad[:8], got[r][bad[:8]], want[bad[:8]])
-    assert np.all(status.cpu().numpy() == 0)
+        assert len(bad) == 0, (rows[r], bad[:8], got[r][bad[:8]], want[bad[:8]])
 
 
 def test_processors_f32():
