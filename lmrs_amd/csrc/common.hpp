@@ -51,98 +51,153 @@ __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float(u);
 }
 
+// ---- uniform values -------------------------------------------------------
+// Values that every lane holds identically (block reductions, LDS
+// broadcasts) are moved to scalar registers, so that branches on them are
+// uniform to the compiler as well: an early return then really leaves, and
+// values live only on the other side of a branch do not stay live across it.
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int32_t uniform(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uniform(float v) {
+  return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v)));
+}
+__device__ __forceinline__ uint64_t uniform(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ int64_t uniform(int64_t v) { return (int64_t)uniform((uint64_t)v); }
+__device__ __forceinline__ double uniform(double v) {
+  return __longlong_as_double((long long)uniform((uint64_t)__double_as_longlong(v)));
+}
+
 // ---- wave / block collectives ----------------------------------------------
+// Wave-level steps use DPP lane moves (row_shr within rows of 16 lanes, then
+// row_bcast:15 / row_bcast:31 across rows), which complete in a few cycles,
+// instead of LDS-routed shuffles.  Lanes a DPP move cannot source keep `old`
+// (bound_ctrl off), which is chosen as the operation's identity.
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWMASK, 0xF, false);
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T w = __shfl_xor(v, o, 64);
-    v = w > v ? w : v;
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x142, kRowBcast31 = 0x143;
+
+struct OpSum {
+  template <class T> __device__ static T apply(T a, T b) { return a + b; }
+};
+struct OpMax {
+  template <class T> __device__ static T apply(T a, T b) { return a > b ? a : b; }
+};
+struct OpMin {
+  template <class T> __device__ static T apply(T a, T b) { return a < b ? a : b; }
+};
+
+template <class T>
+struct Bits;
+template <>
+struct Bits<uint32_t> {
+  template <int C, int M = 0xF>
+  __device__ static uint32_t mov(uint32_t old, uint32_t v) { return dpp_mov<C, M>(old, v); }
+};
+template <>
+struct Bits<int32_t> {
+  template <int C, int M = 0xF>
+  __device__ static int32_t mov(int32_t old, int32_t v) { return (int32_t)dpp_mov<C, M>((uint32_t)old, (uint32_t)v); }
+};
+template <>
+struct Bits<uint64_t> {
+  template <int C, int M = 0xF>
+  __device__ static uint64_t mov(uint64_t old, uint64_t v) {
+    const uint32_t lo = dpp_mov<C, M>((uint32_t)old, (uint32_t)v);
+    const uint32_t hi = dpp_mov<C, M>((uint32_t)(old >> 32), (uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
   }
+};
+template <>
+struct Bits<double> {
+  template <int C, int M = 0xF>
+  __device__ static double mov(double old, double v) {
+    return __longlong_as_double((long long)Bits<uint64_t>::mov<C, M>((uint64_t)__double_as_longlong(old),
+                                                                      (uint64_t)__double_as_longlong(v)));
+  }
+};
+
+// Inclusive scan across the 64 lanes of a wave (lane 63 holds the total).
+template <class Op, class T>
+__device__ __forceinline__ T wave_inclusive(T v, T id) {
+  v = Op::apply(v, Bits<T>::template mov<kRowShr1>(id, v));
+  v = Op::apply(v, Bits<T>::template mov<kRowShr2>(id, v));
+  v = Op::apply(v, Bits<T>::template mov<kRowShr4>(id, v));
+  v = Op::apply(v, Bits<T>::template mov<kRowShr8>(id, v));
+  v = Op::apply(v, Bits<T>::template mov<kRowBcast15, 0xA>(id, v));
+  v = Op::apply(v, Bits<T>::template mov<kRowBcast31, 0xC>(id, v));
   return v;
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    T w = __shfl_xor(v, o, 64);
-    v = w < v ? w : v;
+template <class T>
+__device__ __forceinline__ T lane63(T v) {
+  if constexpr (sizeof(T) == 8) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  } else {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), 63));
   }
-  return v;
 }
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) { return lane63(wave_inclusive<OpSum>(v, T(0))); }
+template <class T>
+__device__ __forceinline__ T wave_max(T v) { return lane63(wave_inclusive<OpMax>(v, T(0))); }
+__device__ __forceinline__ int32_t wave_max(int32_t v) { return lane63(wave_inclusive<OpMax>(v, (int32_t)0x80000000)); }
+template <class T>
+__device__ __forceinline__ T wave_min(T v) { return lane63(wave_inclusive<OpMin>(v, (T)~T(0))); }
+__device__ __forceinline__ int32_t wave_min(int32_t v) { return lane63(wave_inclusive<OpMin>(v, (int32_t)0x7FFFFFFF)); }
 
 // Block-wide reductions.  `scratch` holds kWaves elements of T; every
-// thread returns the result.  Contains two barriers.
-template <typename T>
-__device__ T block_sum(T v, T *scratch) {
-  v = wave_sum(v);
+// thread returns the (scalar) result.  Contains two barriers.
+template <class Op, class T>
+__device__ __forceinline__ T block_reduce(T w, T *scratch) {
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = w;
   __syncthreads();
   T r = scratch[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) r += scratch[i];
-  return r;
+  for (int i = 1; i < kWaves; ++i) r = Op::apply(r, scratch[i]);
+  return uniform(r);
 }
 
 template <typename T>
-__device__ T block_max(T v, T *scratch) {
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  T r = scratch[0];
-#pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = scratch[i] > r ? scratch[i] : r;
-  return r;
-}
-
+__device__ T block_sum(T v, T *scratch) { return block_reduce<OpSum>(wave_sum(v), scratch); }
 template <typename T>
-__device__ T block_min(T v, T *scratch) {
-  v = wave_min(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
-  __syncthreads();
-  T r = scratch[0];
-#pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = scratch[i] < r ? scratch[i] : r;
-  return r;
-}
+__device__ T block_max(T v, T *scratch) { return block_reduce<OpMax>(wave_max(v), scratch); }
+template <typename T>
+__device__ T block_min(T v, T *scratch) { return block_reduce<OpMin>(wave_min(v), scratch); }
 
 // Exclusive prefix sum over the block in thread order.  Returns the
 // exclusive prefix of `v`; *total receives the block total.  Two barriers.
 template <typename T>
 __device__ T block_exclusive_scan(T v, T *scratch, T *total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  T x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    T y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  const int wave = threadIdx.x >> 6;
+  const T incl = wave_inclusive<OpSum>(v, T(0));
+  const T wtot = lane63(incl);
   __syncthreads();
-  if (lane == 63) scratch[wave] = x;
+  if ((threadIdx.x & 63) == 0) scratch[wave] = wtot;
   __syncthreads();
-  T excl = __shfl_up(x, 1, 64);
-  if (lane == 0) excl = T(0);
   T off = T(0), tot = T(0);
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) {
-    T s = scratch[i];
+    const T s = scratch[i];
     if (i < wave) off += s;
     tot += s;
   }
-  *total = tot;
-  return off + excl;
+  *total = uniform(tot);
+  return off + (incl - v);
 }
 
 }  // namespace lmrs

@@ -1,13 +1,15 @@
-// generic_engine.hpp -- the general-purpose sampling engine (any dtype, any
+// generic_engine.hpp -- the general-purpose selection engine (any dtype, any
 // vocab up to LMRS_MAX_VOCAB, any parameters).
 //
-// One workgroup of 1024 threads owns one row and streams it from memory once
-// per pass (processing every element on the fly).  Selection never sorts the
-// row: it runs radix selections on 32-bit total-order keys with LDS
-// histograms (counts for top-k, counts plus f64 weight sums for the nucleus
-// cut and the inverse-CDF draw) and resolves ties by lowest index with a
-// radix selection on the index.  Small top-k candidate sets are gathered into
-// LDS, sorted exactly and finished with f64 prefix sums.
+// One workgroup of 1024 threads owns one row.  A "row source" supplies, on
+// every pass, the total-order key of each processed element: StreamRow
+// re-reads the row from memory and re-applies the processor chain, RegRow
+// (fast_bf16.hpp) walks keys already held in registers.  Selection never
+// sorts the row: it runs radix selections on 32-bit keys with LDS histograms
+// (counts for top-k, counts plus f64 weight sums for the nucleus cut and the
+// inverse-CDF draw) and resolves ties by lowest index with a radix selection
+// on the index.  Small top-k candidate sets are gathered into LDS, sorted
+// exactly and finished with f64 prefix sums.
 //
 // The order it reproduces is the reference's sorted_logits order: value
 // descending under f32::total_cmp, then index ascending
@@ -46,8 +48,8 @@ struct DTypeTraits<LMRS_DTYPE_F32> {
   __device__ static float value(uint32_t key) { return key_value(key); }
 };
 
-struct GenericShared {
-  HistoryTables ht;
+// LDS working set of the selection routines.
+struct SelState {
   uint32_t bcnt[kBins];
   double bw[kBins];
   uint64_t gather[kGatherCap];
@@ -55,7 +57,6 @@ struct GenericShared {
   uint64_t qscr[kWaves];
   uint32_t uscr[kWaves];
   int32_t iscr[kWaves];
-  RowCfg cfg;
   uint32_t sel[4];
   double dsel[4];
 };
@@ -63,14 +64,18 @@ struct GenericShared {
 // A row streamed from global memory; every pass re-reads and re-processes it.
 template <int DT>
 struct StreamRow {
+  using TR = DTypeTraits<DT>;
   const void *base;
   int64_t vocab;
   bool vec;  // 16-byte aligned rows use dwordx4 loads
+  const RowCfg *cfg;
+  const HistoryTables *ht;
 
   // Calls f(index, key) for every element, key = total-order key of the
   // processed value (bf16 keys keep only their upper 16 bits).
   template <class F>
-  __device__ __forceinline__ void for_each(const RowCfg &c, const HistoryTables &ht, F &&f) const {
+  __device__ __forceinline__ void for_each(F &&f) const {
+    const RowCfg &c = *cfg;
     if constexpr (DT == LMRS_DTYPE_BF16) {
       const uint16_t *p = (const uint16_t *)base;
       int64_t done = 0;
@@ -84,14 +89,14 @@ struct StreamRow {
           for (int e = 0; e < 8; ++e) {
             uint32_t raw = (w[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
             uint32_t idx = (uint32_t)(ch * 8 + e);
-            uint32_t y = process_bf16(raw, idx, c, ht);
+            uint32_t y = process_bf16(raw, idx, c, *ht);
             f(idx, order_key(bf16_to_f32(y)) & 0xFFFF0000u);
           }
         }
         done = nch << 3;
       }
       for (int64_t i = done + threadIdx.x; i < vocab; i += kThreads) {
-        uint32_t y = process_bf16(p[i], (uint32_t)i, c, ht);
+        uint32_t y = process_bf16(p[i], (uint32_t)i, c, *ht);
         f((uint32_t)i, order_key(bf16_to_f32(y)) & 0xFFFF0000u);
       }
     } else {
@@ -106,13 +111,13 @@ struct StreamRow {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             uint32_t idx = (uint32_t)(ch * 4 + e);
-            f(idx, order_key(process_f32(w[e], idx, c, ht)));
+            f(idx, order_key(process_f32(w[e], idx, c, *ht)));
           }
         }
         done = nch << 2;
       }
       for (int64_t i = done + threadIdx.x; i < vocab; i += kThreads)
-        f((uint32_t)i, order_key(process_f32(p[i], (uint32_t)i, c, ht)));
+        f((uint32_t)i, order_key(process_f32(p[i], (uint32_t)i, c, *ht)));
     }
   }
 };
@@ -126,44 +131,43 @@ struct CountSel {
 // k-th largest of val over the included elements (1 <= k <= included count),
 // by radix selection on `total_bits` bits, most significant digit first.
 // vf(index, key, &val) -> bool include.
-template <int DT, class VF>
-__device__ CountSel select_kth_largest(GenericShared &sh, const StreamRow<DT> &row, const RowCfg &c,
-                                       VF vf, uint32_t k, int total_bits, const int *widths,
-                                       int nlev) {
+template <class Row, class VF>
+__device__ __forceinline__ CountSel select_kth_largest(SelState &ss, const Row &row, VF vf, uint32_t k,
+                                                       int total_bits, const int *widths, int nlev) {
   uint32_t prefix = 0, krem = k, ngt = 0, neq = 0;
   int fixed = 0;
   for (int lev = 0; lev < nlev; ++lev) {
     const int w = widths[lev];
     const int shift = total_bits - fixed - w;
     const uint32_t nb = 1u << w;
-    for (uint32_t i = threadIdx.x; i < nb; i += kThreads) sh.bcnt[i] = 0u;
+    for (uint32_t i = threadIdx.x; i < nb; i += kThreads) ss.bcnt[i] = 0u;
     __syncthreads();
-    row.for_each(c, sh.ht, [&](uint32_t idx, uint32_t key) {
+    row.for_each([&](uint32_t idx, uint32_t key) {
       uint32_t val;
       if (!vf(idx, key, val)) return;
       if (fixed != 0 && (val >> (total_bits - fixed)) != prefix) return;
-      atomicAdd(&sh.bcnt[(val >> shift) & (nb - 1u)], 1u);
+      atomicAdd(&ss.bcnt[(val >> shift) & (nb - 1u)], 1u);
     });
     __syncthreads();
     // Bins in descending digit order: thread t owns digits nb-1-2t, nb-2-2t.
     const int d0 = (int)nb - 1 - 2 * (int)threadIdx.x, d1 = d0 - 1;
-    const uint32_t c0 = d0 >= 0 ? sh.bcnt[d0] : 0u, c1 = d1 >= 0 ? sh.bcnt[d1] : 0u;
+    const uint32_t c0 = d0 >= 0 ? ss.bcnt[d0] : 0u, c1 = d1 >= 0 ? ss.bcnt[d1] : 0u;
     uint32_t tot;
-    const uint32_t above0 = block_exclusive_scan(c0 + c1, sh.uscr, &tot);
+    const uint32_t above0 = block_exclusive_scan(c0 + c1, ss.uscr, &tot);
     const uint32_t above1 = above0 + c0;
     if (d0 >= 0 && c0 > 0 && above0 < krem && krem <= above0 + c0) {
-      sh.sel[0] = (uint32_t)d0;
-      sh.sel[1] = above0;
-      sh.sel[2] = c0;
+      ss.sel[0] = (uint32_t)d0;
+      ss.sel[1] = above0;
+      ss.sel[2] = c0;
     }
     if (d1 >= 0 && c1 > 0 && above1 < krem && krem <= above1 + c1) {
-      sh.sel[0] = (uint32_t)d1;
-      sh.sel[1] = above1;
-      sh.sel[2] = c1;
+      ss.sel[0] = (uint32_t)d1;
+      ss.sel[1] = above1;
+      ss.sel[2] = c1;
     }
     __syncthreads();
-    const uint32_t d = sh.sel[0], above = sh.sel[1];
-    neq = sh.sel[2];
+    const uint32_t d = uniform(ss.sel[0]), above = uniform(ss.sel[1]);
+    neq = uniform(ss.sel[2]);
     krem -= above;
     ngt += above;
     prefix = (prefix << w) | d;
@@ -192,11 +196,12 @@ struct WeightSel {
 // cumulative weight reaches frac * (kept mass).  Kept set: keys >= low_key,
 // minus `clamp_excess` elements at key == clamp_key (those with the highest
 // indices; their weights equal the others' at that key).
-template <int DT>
-__device__ WeightSel select_by_weight(GenericShared &sh, const StreamRow<DT> &row, const RowCfg &c,
-                                      double frac, uint32_t low_key, bool clamp_on,
-                                      uint32_t clamp_key, uint32_t clamp_excess, float M) {
-  using TR = DTypeTraits<DT>;
+template <class Row>
+__device__ __forceinline__ WeightSel select_by_weight(SelState &ss, const Row &row, double frac,
+                                                      uint32_t low_key, bool clamp_on,
+                                                      uint32_t clamp_key, uint32_t clamp_excess,
+                                                      float M) {
+  using TR = typename Row::TR;
   uint32_t prefix = 0;
   int fixed = 0;
   double target = 0.0, above_acc = 0.0, total = 0.0;
@@ -208,31 +213,31 @@ __device__ WeightSel select_by_weight(GenericShared &sh, const StreamRow<DT> &ro
     const int shift = 32 - fixed - w;
     const uint32_t nb = 1u << w;
     for (uint32_t i = threadIdx.x; i < nb; i += kThreads) {
-      sh.bcnt[i] = 0u;
-      sh.bw[i] = 0.0;
+      ss.bcnt[i] = 0u;
+      ss.bw[i] = 0.0;
     }
     __syncthreads();
-    row.for_each(c, sh.ht, [&](uint32_t idx, uint32_t key) {
+    row.for_each([&](uint32_t idx, uint32_t key) {
       (void)idx;
       if (key < low_key) return;
       if (fixed != 0 && (key >> (32 - fixed)) != prefix) return;
       const uint32_t d = (key >> shift) & (nb - 1u);
-      atomicAdd(&sh.bcnt[d], 1u);
-      atomicAdd(&sh.bw[d], (double)expf(TR::value(key) - M));
+      atomicAdd(&ss.bcnt[d], 1u);
+      atomicAdd(&ss.bw[d], (double)expf(TR::value(key) - M));
     });
     __syncthreads();
     if (threadIdx.x == 0 && clamp_on && clamp_excess > 0u &&
         (fixed == 0 || (clamp_key >> (32 - fixed)) == prefix)) {
       const uint32_t d = (clamp_key >> shift) & (nb - 1u);
-      sh.bcnt[d] -= clamp_excess;
-      sh.bw[d] -= (double)clamp_excess * (double)expf(TR::value(clamp_key) - M);
+      ss.bcnt[d] -= clamp_excess;
+      ss.bw[d] -= (double)clamp_excess * (double)expf(TR::value(clamp_key) - M);
     }
     __syncthreads();
     const int d0 = (int)nb - 1 - 2 * (int)threadIdx.x, d1 = d0 - 1;
-    const uint32_t c0 = d0 >= 0 ? sh.bcnt[d0] : 0u, c1 = d1 >= 0 ? sh.bcnt[d1] : 0u;
-    const double w0 = d0 >= 0 ? sh.bw[d0] : 0.0, w1 = d1 >= 0 ? sh.bw[d1] : 0.0;
+    const uint32_t c0 = d0 >= 0 ? ss.bcnt[d0] : 0u, c1 = d1 >= 0 ? ss.bcnt[d1] : 0u;
+    const double w0 = d0 >= 0 ? ss.bw[d0] : 0.0, w1 = d1 >= 0 ? ss.bw[d1] : 0.0;
     double tot;
-    const double above0 = block_exclusive_scan(w0 + w1, sh.dscr, &tot);
+    const double above0 = block_exclusive_scan(w0 + w1, ss.dscr, &tot);
     const double above1 = above0 + w0;
     if (lev == 0) {
       total = tot;
@@ -246,24 +251,24 @@ __device__ WeightSel select_by_weight(GenericShared &sh, const StreamRow<DT> &ro
     int last = -1;
     if (d1 >= 0 && c1 > 0) last = 2 * (int)threadIdx.x + 1;
     else if (d0 >= 0 && c0 > 0) last = 2 * (int)threadIdx.x;
-    pos = block_min(pos, sh.iscr);
-    last = block_max(last, sh.iscr);
+    pos = block_min(pos, ss.iscr);
+    last = block_max(last, ss.iscr);
     const bool ovf = pos == 0x7FFFFFFF;
     const int pick = ovf ? last : pos;
     if ((int)threadIdx.x == pick / 2) {
       const bool first = (pick & 1) == 0;
-      sh.sel[0] = (uint32_t)(first ? d0 : d1);
-      sh.sel[1] = first ? c0 : c1;
-      sh.dsel[0] = first ? above0 : above1;
-      sh.dsel[1] = first ? w0 : w1;
+      ss.sel[0] = (uint32_t)(first ? d0 : d1);
+      ss.sel[1] = first ? c0 : c1;
+      ss.dsel[0] = first ? above0 : above1;
+      ss.dsel[1] = first ? w0 : w1;
     }
     __syncthreads();
-    const uint32_t d = sh.sel[0];
-    sel_n = sh.sel[1];
-    const double above = sh.dsel[0];
+    const uint32_t d = uniform(ss.sel[0]);
+    sel_n = uniform(ss.sel[1]);
+    const double above = uniform(ss.dsel[0]);
     if (ovf) {
       r.overflow = true;
-      target = above + sh.dsel[1];  // lands on the bin's last element
+      target = above + uniform(ss.dsel[1]);  // lands on the bin's last element
     }
     target -= above;
     above_acc += above;
@@ -293,59 +298,54 @@ __device__ __forceinline__ void write_row(const lmrs_sample_args &a, int r, uint
   if (a.status) a.status[r] = status;
 }
 
-// Finishes a row whose top-k candidates (keys >= tk, n of them) fit the
-// gather buffer: exact sort by (key desc, index asc), then the nucleus cut
-// (top_p.rs:45-58) and softmax_choice (strategies/mod.rs:27-55) with f64
-// weights exp(f64(l - max)) and prefix sums.
-template <int DT>
-__device__ void finish_small_k(GenericShared &sh, const StreamRow<DT> &row, const RowCfg &c,
-                               const lmrs_sample_args &a, int r, uint32_t tk, uint32_t n,
-                               uint32_t k) {
-  using TR = DTypeTraits<DT>;
-  if (threadIdx.x == 0) sh.sel[3] = 0u;
-  __syncthreads();
-  row.for_each(c, sh.ht, [&](uint32_t idx, uint32_t key) {
-    if (key < tk) return;
-    const uint32_t s = atomicAdd(&sh.sel[3], 1u);
-    sh.gather[s] = ((uint64_t)(~key) << 32) | (uint64_t)idx;
-  });
-  __syncthreads();
+// Sorts ss.gather[0..n) ascending (bitonic; n <= kGatherCap).  Barriers inside.
+__device__ __forceinline__ void sort_gather(SelState &ss, uint32_t n) {
   uint32_t n2 = 1;
   while (n2 < n) n2 <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < n2; i += kThreads) sh.gather[i] = ~0ull;
+  for (uint32_t i = n + threadIdx.x; i < n2; i += kThreads) ss.gather[i] = ~0ull;
   __syncthreads();
   for (uint32_t kk = 2; kk <= n2; kk <<= 1) {
     for (uint32_t jj = kk >> 1; jj > 0; jj >>= 1) {
       for (uint32_t i = threadIdx.x; i < n2; i += kThreads) {
         const uint32_t ixj = i ^ jj;
         if (ixj > i) {
-          const uint64_t x = sh.gather[i], y = sh.gather[ixj];
+          const uint64_t x = ss.gather[i], y = ss.gather[ixj];
           const bool asc = (i & kk) == 0;
           if ((x > y) == asc) {
-            sh.gather[i] = y;
-            sh.gather[ixj] = x;
+            ss.gather[i] = y;
+            ss.gather[ixj] = x;
           }
         }
       }
       __syncthreads();
     }
   }
+}
+
+// Finishes a row from its sorted candidate list: ss.gather[0..k) holds
+// ((~key) << 32 | index) in ascending order, i.e. the reference's sorted
+// order.  Applies the nucleus cut (top_p.rs:45-58) and softmax_choice
+// (strategies/mod.rs:27-55) with f64 weights exp(f64(l - max)) and f64
+// prefix sums, and writes the outputs.
+template <class TR>
+__device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, const lmrs_sample_args &a,
+                                              int r, uint32_t k) {
   // Thread t owns sorted entries 4t .. 4t+3 of the first k.
-  const float M = TR::value(~(uint32_t)(sh.gather[0] >> 32));
+  const float M = TR::value(~uniform((uint32_t)(ss.gather[0] >> 32)));
   double wv[4], incl[4], local = 0.0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
     wv[q] = 0.0;
     if (i < k) {
-      const float y = TR::value(~(uint32_t)(sh.gather[i] >> 32));
+      const float y = TR::value(~(uint32_t)(ss.gather[i] >> 32));
       wv[q] = exp((double)(y - M));
     }
     local += wv[q];
     incl[q] = local;
   }
   double sum_all;
-  const double excl = block_exclusive_scan(local, sh.dscr, &sum_all);
+  const double excl = block_exclusive_scan(local, ss.dscr, &sum_all);
 #pragma unroll
   for (int q = 0; q < 4; ++q) incl[q] += excl;
   if (!(__builtin_isfinite(sum_all) && sum_all > 0.0)) {
@@ -361,7 +361,7 @@ __device__ void finish_small_k(GenericShared &sh, const StreamRow<DT> &row, cons
       const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
       if (i < k && incl[q] / sum_all >= c.top_p) first = (int)i;
     }
-    first = block_min(first, sh.iscr);
+    first = block_min(first, ss.iscr);
     if (first != 0x7FFFFFFF) keep = (uint32_t)first + 1u;
     // nucleus margin at the cut
 #pragma unroll
@@ -372,18 +372,18 @@ __device__ void finish_small_k(GenericShared &sh, const StreamRow<DT> &row, cons
         double m = c.top_p - prev;
         if (acc >= c.top_p && acc - c.top_p < m) m = acc - c.top_p;
         if (!(acc >= c.top_p)) m = c.top_p - acc;
-        sh.dsel[2] = m;
+        ss.dsel[2] = m;
       }
     }
     __syncthreads();
-    if (sh.dsel[2] < 1e-6) flags |= LMRS_ROW_NEAR_BOUNDARY;
+    if (uniform(ss.dsel[2]) < 1e-6) flags |= LMRS_ROW_NEAR_BOUNDARY;
   }
   // sum over the kept prefix, held by the owner of entry keep-1
 #pragma unroll
   for (int q = 0; q < 4; ++q)
-    if (4u * threadIdx.x + (uint32_t)q + 1u == keep) sh.dsel[3] = incl[q];
+    if (4u * threadIdx.x + (uint32_t)q + 1u == keep) ss.dsel[3] = incl[q];
   __syncthreads();
-  const double sum_keep = sh.dsel[3];
+  const double sum_keep = uniform(ss.dsel[3]);
   const double target = c.u * sum_keep;
   int pick = 0x7FFFFFFF;
 #pragma unroll
@@ -391,13 +391,13 @@ __device__ void finish_small_k(GenericShared &sh, const StreamRow<DT> &row, cons
     const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
     if (i < keep && target <= incl[q]) pick = (int)i;
   }
-  pick = block_min(pick, sh.iscr);
+  pick = block_min(pick, ss.iscr);
   if (pick == 0x7FFFFFFF) pick = (int)keep - 1;  // fallback: last candidate (mod.rs:52-54)
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
     if ((int)i == pick) {
-      const uint64_t g = sh.gather[i];
+      const uint64_t g = ss.gather[i];
       const uint32_t token = (uint32_t)(g & 0xFFFFFFFFu);
       const float y = TR::value(~(uint32_t)(g >> 32));
       const double lo = (incl[q] - wv[q]) / sum_keep, hi = incl[q] / sum_keep;
@@ -410,41 +410,32 @@ __device__ void finish_small_k(GenericShared &sh, const StreamRow<DT> &row, cons
   }
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_args a, int vec) {
-  using TR = DTypeTraits<DT>;
-  __shared__ GenericShared sh;
-  const int r = blockIdx.x;
-  if (threadIdx.x == 0) sh.cfg = load_row_cfg(a, r, DT);
+// Finishes a row whose top-k candidates (keys >= tk, n of them) fit the
+// gather buffer: gather, exact sort by (key desc, index asc), finish.
+template <class Row>
+__device__ __forceinline__ void finish_small_k(SelState &ss, const Row &row, const RowCfg &c,
+                                               const lmrs_sample_args &a, int r, uint32_t tk,
+                                               uint32_t n, uint32_t k) {
+  if (threadIdx.x == 0) ss.sel[3] = 0u;
   __syncthreads();
-  const RowCfg c = sh.cfg;
-  const int64_t V = a.vocab;
-  if (c.status != LMRS_ROW_OK || V == 0) {
-    if (threadIdx.x == 0)
-      write_row(a, r, 0u, 0.0f, 0.0f, c.status != LMRS_ROW_OK ? c.status : LMRS_ROW_EMPTY);
-    return;
-  }
-  if (c.hist_on) build_history(sh.ht, a, c, V);
-  StreamRow<DT> row;
-  row.base = (const char *)a.logits + (size_t)r * (size_t)a.row_stride * TR::kElemBytes;
-  row.vocab = V;
-  row.vec = vec != 0;
-
-  // Pass 1: maximum (total order), lowest index at the maximum, and the
-  // number of negative NaNs (which sort below -inf).
-  uint64_t best = 0;
-  uint32_t nneg = 0;
-  row.for_each(c, sh.ht, [&](uint32_t idx, uint32_t key) {
-    const uint64_t pk = ((uint64_t)key << 32) | (uint64_t)(~idx);
-    best = pk > best ? pk : best;
-    nneg += key < TR::kNegInfKey ? 1u : 0u;
+  row.for_each([&](uint32_t idx, uint32_t key) {
+    if (key < tk) return;
+    const uint32_t s = atomicAdd(&ss.sel[3], 1u);
+    ss.gather[s] = ((uint64_t)(~key) << 32) | (uint64_t)idx;
   });
-  best = block_max(best, sh.qscr);
-  nneg = block_sum(nneg, sh.uscr);
-  const uint32_t kmax = (uint32_t)(best >> 32);
-  const uint32_t imax = ~(uint32_t)(best & 0xFFFFFFFFu);
-  const float M = TR::value(kmax);
+  __syncthreads();
+  sort_gather(ss, n);
+  finish_sorted<typename Row::TR>(ss, c, a, r, k);
+}
 
+// The whole selection for one row from any row source: greedy, top-k,
+// nucleus cut and draw.  kmax/imax/nneg come from the caller's stats pass.
+template <class Row>
+__device__ __forceinline__ void select_row(SelState &ss, const Row &row, const RowCfg &c,
+                                           const lmrs_sample_args &a, int r, int64_t V,
+                                           uint32_t kmax, uint32_t imax, uint32_t nneg) {
+  using TR = typename Row::TR;
+  const float M = TR::value(kmax);
   if (c.top_k == 1) {  // Greedy (greedy.rs:22-29): sorted[0], log_prob 0
     if (threadIdx.x == 0) write_row(a, r, imax, 0.0f, M, LMRS_ROW_OK);
     return;
@@ -460,8 +451,8 @@ __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_ar
 
   uint32_t tk = 0u, needed = 0u, neq_k = 0u;
   if (k_on) {
-    const CountSel s = select_kth_largest<DT>(
-        sh, row, c,
+    const CountSel s = select_kth_largest(
+        ss, row,
         [](uint32_t, uint32_t key, uint32_t &val) {
           val = key;
           return true;
@@ -471,7 +462,7 @@ __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_ar
     needed = (uint32_t)c.top_k - s.n_gt;
     neq_k = s.n_eq;
     if (s.n_gt + s.n_eq <= (uint32_t)kGatherCap) {
-      finish_small_k<DT>(sh, row, c, a, r, tk, s.n_gt + s.n_eq, (uint32_t)c.top_k);
+      finish_small_k(ss, row, c, a, r, tk, s.n_gt + s.n_eq, (uint32_t)c.top_k);
       return;
     }
   }
@@ -482,8 +473,8 @@ __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_ar
   uint32_t kept_ckey = tk, kept_excess = k_on ? neq_k - needed : 0u;
   int32_t flags = 0;
   if (c.top_p < 1.0) {
-    const WeightSel p = select_by_weight<DT>(sh, row, c, c.top_p, kept_low, kept_clamp, kept_ckey,
-                                             kept_excess, M);
+    const WeightSel p =
+        select_by_weight(ss, row, c.top_p, kept_low, kept_clamp, kept_ckey, kept_excess, M);
     const double denom = p.total;
     if (p.overflow) {
       // the nucleus cumulative never reached top_p: everything is kept
@@ -500,13 +491,12 @@ __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_ar
       kept_excess = p.n_full - p.j;
     }
   }
-  const WeightSel d = select_by_weight<DT>(sh, row, c, c.u, kept_low, kept_clamp, kept_ckey,
-                                           kept_excess, M);
+  const WeightSel d = select_by_weight(ss, row, c.u, kept_low, kept_clamp, kept_ckey, kept_excess, M);
   // The d.j-th lowest index among elements with key d.key.
   const uint32_t want = d.key;
   const int idx_w[2] = {11, 7};
-  const CountSel s = select_kth_largest<DT>(
-      sh, row, c,
+  const CountSel s = select_kth_largest(
+      ss, row,
       [want](uint32_t idx, uint32_t key, uint32_t &val) {
         val = 0x3FFFFu - idx;
         return key == want;
@@ -524,6 +514,78 @@ __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_ar
     if (d.overflow) m = 0.0;
     const int32_t st = flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0);
     write_row(a, r, token, (float)log(w_exact / d.total), y, st);
+  }
+}
+
+// Stats pass: maximum key (total order), lowest index at the maximum, and the
+// number of negative NaNs (which sort below -inf).
+template <class Row>
+__device__ __forceinline__ void row_stats(SelState &ss, const Row &row, uint32_t &kmax,
+                                          uint32_t &imax, uint32_t &nneg) {
+  using TR = typename Row::TR;
+  uint64_t best = 0;
+  uint32_t neg = 0;
+  row.for_each([&](uint32_t idx, uint32_t key) {
+    const uint64_t pk = ((uint64_t)key << 32) | (uint64_t)(~idx);
+    best = pk > best ? pk : best;
+    neg += key < TR::kNegInfKey ? 1u : 0u;
+  });
+  best = block_max(best, ss.qscr);
+  nneg = block_sum(neg, ss.uscr);
+  kmax = (uint32_t)(best >> 32);
+  imax = ~(uint32_t)(best & 0xFFFFFFFFu);
+}
+
+struct GenericShared {
+  HistoryTables ht;
+  SelState ss;
+  RowCfg cfg;
+};
+
+// Token id the fast kernels write for rows they leave to the generic pass.
+constexpr uint32_t kDeferred = 0xFFFFFFFFu;
+
+// One row through the generic engine (all threads of the workgroup).
+template <int DT>
+__device__ __forceinline__ void generic_row(GenericShared &sh, const lmrs_sample_args &a, int r, int vec) {
+  using TR = DTypeTraits<DT>;
+  if (threadIdx.x == 0) sh.cfg = load_row_cfg(a, r, DT);
+  __syncthreads();
+  const RowCfg c = uniform_cfg(sh.cfg);
+  const int64_t V = a.vocab;
+  if (c.status != LMRS_ROW_OK || V == 0) {
+    if (threadIdx.x == 0)
+      write_row(a, r, 0u, 0.0f, 0.0f, c.status != LMRS_ROW_OK ? c.status : LMRS_ROW_EMPTY);
+    return;
+  }
+  if (c.hist_on) build_history(sh.ht, a, c, V);
+  StreamRow<DT> row;
+  row.base = (const char *)a.logits + (size_t)r * (size_t)a.row_stride * TR::kElemBytes;
+  row.vocab = V;
+  row.vec = vec != 0;
+  row.cfg = &sh.cfg;
+  row.ht = &sh.ht;
+  uint32_t kmax, imax, nneg;
+  row_stats(sh.ss, row, kmax, imax, nneg);
+  select_row(sh.ss, row, c, a, r, V, kmax, imax, nneg);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_args a, int vec) {
+  __shared__ GenericShared sh;
+  generic_row<DT>(sh, a, blockIdx.x, vec);
+}
+
+// Finishes the rows a fast kernel marked kDeferred (launched right after it
+// on the same stream); a few workgroups stride over the batch.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) generic_deferred_kernel(lmrs_sample_args a, int vec) {
+  __shared__ GenericShared sh;
+  for (int r = blockIdx.x; r < a.batch; r += gridDim.x) {
+    if (a.token_ids[r] != kDeferred) continue;  // same address for every thread: uniform
+    __syncthreads();
+    generic_row<DT>(sh, a, r, vec);
+    __syncthreads();
   }
 }
 

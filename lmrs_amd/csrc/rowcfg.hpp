@@ -8,7 +8,7 @@
 // same ops without rounding.
 #pragma once
 
-#include "../../include/lmrs_sampling.h"
+#include "lmrs_sampling.h"
 #include "common.hpp"
 
 namespace lmrs {
@@ -54,6 +54,27 @@ __device__ __forceinline__ uint32_t history_count(const HistoryTables &ht, uint3
 
 __device__ __forceinline__ bool history_member(const HistoryTables &ht, uint32_t i) {
   return (ht.bitmap[i >> 5] >> (i & 31u)) & 1u;
+}
+
+// Every field through a scalar register (see uniform()).
+__device__ inline RowCfg uniform_cfg(const RowCfg &s) {
+  RowCfg c;
+  c.status = uniform((int32_t)s.status);
+  c.rep_on = uniform((int32_t)s.rep_on);
+  c.pres_on = uniform((int32_t)s.pres_on);
+  c.temp_on = uniform((int32_t)s.temp_on);
+  c.hist_on = uniform((int32_t)s.hist_on);
+  c.pf = uniform(s.pf);
+  c.nf = uniform(s.nf);
+  c.presence = uniform(s.presence);
+  c.frequency = uniform(s.frequency);
+  c.scale = uniform(s.scale);
+  c.top_k = uniform(s.top_k);
+  c.top_p = uniform(s.top_p);
+  c.u = uniform(s.u);
+  c.h_begin = uniform(s.h_begin);
+  c.h_len = uniform(s.h_len);
+  return c;
 }
 
 // Reads and validates row r's parameters (thread 0 only).  Validation

@@ -2,10 +2,14 @@
 //
 // Host-side argument checks, then one launch of one workgroup per row on the
 // caller's stream.  Nothing here allocates device memory.
-#include "../../include/lmrs_sampling.h"
+#include "lmrs_sampling.h"
+#include "fast_bf16.hpp"
 #include "generic_engine.hpp"
 
 namespace {
+
+// Workgroups of the pass that finishes deferred rows.
+constexpr int kDeferredGrid = 64;
 
 int check_args(const lmrs_sample_args *a, bool need_tokens) {
   if (!a) return LMRS_ERR_NULL_ARGUMENT;
@@ -33,7 +37,22 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
   if (st != LMRS_OK || args->batch == 0) return st;
   hipStream_t s = (hipStream_t)stream;
   const int vec = vector_ok(args);
-  if (args->dtype == LMRS_DTYPE_BF16)
+  const int64_t V = args->vocab;
+  if (args->dtype == LMRS_DTYPE_BF16 && vec && V > 0 && V % 8 == 0 && V <= lmrs::kFastMaxVocab) {
+    // register-resident rows: NCH chunks of 8 logits per thread, then the
+    // generic pass for the rows the fast kernel deferred
+    const dim3 grid(args->batch), block(lmrs::kThreads);
+    if (V <= 4 * 8192)
+      lmrs::bf16_fast_kernel<4><<<grid, block, 0, s>>>(*args);
+    else if (V <= 8 * 8192)
+      lmrs::bf16_fast_kernel<8><<<grid, block, 0, s>>>(*args);
+    else if (V <= 16 * 8192)
+      lmrs::bf16_fast_kernel<16><<<grid, block, 0, s>>>(*args);
+    else
+      lmrs::bf16_fast_kernel<20><<<grid, block, 0, s>>>(*args);
+    const int g2 = args->batch < kDeferredGrid ? args->batch : kDeferredGrid;
+    lmrs::generic_deferred_kernel<LMRS_DTYPE_BF16><<<g2, lmrs::kThreads, 0, s>>>(*args, vec);
+  } else if (args->dtype == LMRS_DTYPE_BF16)
     lmrs::generic_sample_kernel<LMRS_DTYPE_BF16><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
   else
     lmrs::generic_sample_kernel<LMRS_DTYPE_F32><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
