@@ -1,0 +1,228 @@
+"""Benchmark of the batched sampling step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
+
+A step is one call of ``lmrs_sample_fwd`` (the C-ABI entry point) over the
+whole batch of the configuration: penalties, temperature, top-k, top-p and the
+draw for every row, logits already resident in HBM.  The logits are generated
+once (synthetic, seeded) and replicated into enough rotating buffers that the
+rotation exceeds the 256 MB last-level (MALL) cache, so every step streams its
+logits from HBM.  The timed region is bracketed by HIP events recorded on the
+stream the kernels are launched on.
+
+Prints one JSON line: rows/s of the whole job, microseconds per step, the HBM
+roofline of the step (algorithmic bytes / step time against 8 TB/s; measured
+HBM traffic per launch from the committed rocprofv3 counter summary) and the
+CPU baseline: the C restatement of the reference's CPU sampler timed on this
+host's cores on a bounded sample of the same rows, whose tokens are also
+compared with the GPU's.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak
+LLC_BYTES = 256 << 20  # MI355X Infinity Cache (MALL)
+METRIC = "sampled rows/sec + µs/step + % HBM peak, batch 256 × vocab 128256 bf16"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_bf16_fast_kernel_C3.txt")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def workload_config(w) -> dict:
+    desc = {
+        "C1": "C1: batch 1 x vocab 32000 f32, T=0.8, top_k=50, top_p=0.9",
+        "C2": "C2: batch 64 x vocab 128256 bf16 Student-t, per-row T, top_k, top_p",
+        "C3": ("C3: batch 256 x vocab 128256 bf16 N(0,2.5^2), history 2048 Zipf(1.1) ids/row, "
+               "repetition 1.1, presence 0.5, frequency 0.3, T=0.7, top_k=50, top_p=0.95"),
+        "C4": "C4: batch 1024 x vocab 151936 bf16, half greedy, half full multinomial",
+        "C5": "C5: batch 512 x vocab 256000 f32, top_p=0.99, repetition 1.05 over 512 ids/row",
+    }[w.name]
+    return {"workload": desc, "batch": w.batch, "vocab": w.vocab, "logits_dtype": w.dtype,
+            "history_per_row": w.hist_len}
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from the committed counter summary (None if absent)."""
+    if name != "C3" or not os.path.exists(TRAFFIC_FILE):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*([0-9.]+)", open(TRAFFIC_FILE).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, gpu_out, seconds: float):
+    """Times the oracle (the C restatement of the reference's CPU sampler) on
+    the workload's rows for about `seconds` of wall time, and compares its
+    tokens with the GPU's."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from helpers import compare, run_oracle
+
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(16, cores))
+    # one pass over the batch, repeated until about `seconds` of wall time
+    t0 = time.perf_counter()
+    ref = run_oracle(w, threads=threads)
+    passes, dt = 1, time.perf_counter() - t0
+    while dt < seconds:
+        run_oracle(w, threads=threads)
+        passes += 1
+        dt = time.perf_counter() - t0
+    n = w.batch
+    gpu = {k: v[:n] for k, v in gpu_out.items()}
+    rep = compare(gpu, ref)
+    base = {"value": passes * n / dt, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} passes over all {n} rows of {w.name} ({dt:.1f} s, {threads} threads, "
+                      f"oracle/lmrs_oracle.c sample_batch, one row per thread at a time)"}
+    parity = {k: rep[k] for k in ("rows", "status_mismatch", "token_mismatch", "boundary_rows",
+                                  "boundary_mismatch", "logit_mismatch", "max_prob_rel_err")}
+    return base, parity
+
+
+def copy_calibration(size_mb: int, reps: int) -> None:
+    """A plain device copy of known size, for scaling the FETCH_SIZE /
+    WRITE_SIZE counters to bytes (run under rocprofv3 --pmc)."""
+    import torch
+
+    n = size_mb << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}), flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, metavar="MB", default=0,
+                    help="run only a device copy of MB megabytes (counter calibration)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} (WORLD_SIZE {world}) is not supported; "
+              "the sampling step has no cross-GPU part (rows are independent) -- run with --gpus 1",
+              file=sys.stderr, flush=True)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration, max(1, args.steps))
+        return 0
+
+    from lmrs_amd import sampling as S
+    from lmrs_amd import workloads as W
+
+    S.lib()  # fails loudly when the HIP library is not built
+    w = W.CONFIGS[args.config]()
+    log(f"bench: {args.config} batch {w.batch} vocab {w.vocab} {w.dtype}")
+    dev = torch.device("cuda", 0)
+    if w.dtype == "bf16":
+        import numpy as np
+
+        base = torch.from_numpy(w.logits.view(np.int16)).view(torch.bfloat16).to(dev)
+    else:
+        base = torch.from_numpy(w.logits).to(dev)
+    nbytes = base.numel() * base.element_size()
+    nrot = max(1, -(-2 * LLC_BYTES // nbytes))  # rotation covers twice the MALL
+    bufs = [base] + [base.clone() for _ in range(nrot - 1)]
+    off = ids = None
+    if w.hist_offsets is not None:
+        import numpy as np
+
+        off = torch.from_numpy(w.hist_offsets.astype(np.int64)).to(dev)
+        ids = torch.from_numpy(w.hist_ids.astype(np.uint32).view(np.int32)).to(dev)
+    params = {k: torch.from_numpy(getattr(w, k)).to(dev) for k in
+              ("repetition_penalty", "presence_penalty", "frequency_penalty", "temperature", "top_k", "top_p",
+               "uniforms")}
+    out = None
+    batches = []
+    for b in bufs:
+        pb = S.prepare_batch(b, hist_offsets=off, hist_ids=ids, out=out, **params)
+        out = pb.out
+        batches.append(pb)
+
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            batches[i % nrot].launch(stream)
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(args.steps):
+            batches[i % nrot].launch(stream)
+        end.record(stream)
+        end.synchronize()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / max(1, args.steps)
+    log(f"bench: {args.steps} steps, {ms * 1e3:.1f} us/step")
+
+    # outputs of the last step (every rotation holds the same logits)
+    res = {
+        "token_id": out["token_ids"].cpu().numpy().view("uint32"),
+        "log_prob": out["log_probs"].cpu().numpy(),
+        "logit": out["logits"].cpu().numpy(),
+        "status": out["status"].cpu().numpy(),
+    }
+    alg = w.algorithmic_bytes()
+    achieved = alg / (ms * 1e-3) / 1e9
+    traffic = read_traffic(w.name)
+    line = {
+        "metric": METRIC,
+        "value": w.batch / (ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "us_per_step": ms * 1e3,
+        "hbm_peak_pct": 100.0 * achieved / HBM_PEAK_GBS,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w.dtype == "bf16" else "f32",
+        "data": "synthetic (seeded generator of the configuration's distributions)",
+        "config": workload_config(w),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes": alg, "kernel": "bf16_fast_kernel + generic_deferred_kernel (one step)"},
+        "rotating_buffers": nrot,
+    }
+    if not args.no_cpu:
+        log("bench: CPU baseline (oracle) ...")
+        line["cpu_baseline"], line["parity_sample"] = cpu_baseline(w, res, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

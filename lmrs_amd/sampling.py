@@ -118,15 +118,27 @@ def history_csr(histories: Sequence[Sequence[int]], device):
     return off_t, ids
 
 
-def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
-                 presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
-                 top_p=None, uniforms=None, stream=None, out=None):
-    """Samples one token per row of a [B, V] bf16/f32 CUDA tensor.
+class PreparedBatch:
+    """A sampling call with its argument block built once: ``launch`` only
+    enqueues the kernels (for callers that repeat a step on fixed buffers)."""
 
-    Per-row parameters are tensors or sequences of length B (None = neutral).
-    Returns dict(token_ids uint32-as-int32, log_probs f32, logits f32, status i32),
-    all on the logits' device; the call is asynchronous on `stream`.
-    """
+    def __init__(self, args: SampleArgs, out: dict, keep: tuple):
+        self.args = args
+        self.out = out
+        self._keep = keep
+
+    def launch(self, stream) -> None:
+        rc = lib().lmrs_sample_fwd(ctypes.byref(self.args), ctypes.c_void_p(stream.cuda_stream))
+        if rc != LMRS_OK:
+            raise SamplingError(f"lmrs_sample_fwd failed with code {rc}")
+
+
+def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
+                  presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
+                  top_p=None, uniforms=None, out=None) -> PreparedBatch:
+    """Validates the host-side shapes and builds the argument block of
+    ``lmrs_sample_fwd`` (per-row parameters as tensors or sequences of length
+    B, None = neutral)."""
     torch = _torch()
     if logits.dim() != 2:
         raise ValueError("logits must be [batch, vocab]")
@@ -156,12 +168,28 @@ def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty
         _ptr(hist_offsets), _ptr(hist_ids), _ptr(rp), _ptr(pp), _ptr(fp), _ptr(tt), _ptr(tk), _ptr(tp), _ptr(uu),
         _ptr(out["token_ids"]), _ptr(out["log_probs"]), _ptr(out["logits"]), _ptr(out["status"]),
     )
-    s = stream if stream is not None else torch.cuda.current_stream(dev)
-    rc = lib().lmrs_sample_fwd(ctypes.byref(args), ctypes.c_void_p(s.cuda_stream))
-    if rc != LMRS_OK:
-        raise SamplingError(f"lmrs_sample_fwd failed with code {rc}")
+    return PreparedBatch(args, out, (logits, rp, pp, fp, tt, tk, tp, uu, hist_offsets, hist_ids))
+
+
+def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
+                 presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
+                 top_p=None, uniforms=None, stream=None, out=None):
+    """Samples one token per row of a [B, V] bf16/f32 CUDA tensor.
+
+    Per-row parameters are tensors or sequences of length B (None = neutral).
+    Returns dict(token_ids uint32-as-int32, log_probs f32, logits f32, status i32),
+    all on the logits' device; the call is asynchronous on `stream`.
+    """
+    torch = _torch()
+    pb = prepare_batch(logits, hist_offsets=hist_offsets, hist_ids=hist_ids,
+                       repetition_penalty=repetition_penalty, presence_penalty=presence_penalty,
+                       frequency_penalty=frequency_penalty, temperature=temperature, top_k=top_k,
+                       top_p=top_p, uniforms=uniforms, out=out)
+    s = stream if stream is not None else torch.cuda.current_stream(logits.device)
+    pb.launch(s)
+    out = pb.out
     # keep argument tensors alive until the stream has consumed them
-    out["_keep"] = (rp, pp, fp, tt, tk, tp, uu, hist_offsets, hist_ids)
+    out["_keep"] = pb._keep
     return out
 
 
