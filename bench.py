@@ -212,7 +212,7 @@ def main() -> int:
         "config": workload_config(w),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "algorithmic_bytes": alg, "kernel": "bf16_fast_kernel + generic_deferred_kernel (one step)"},
+                     "algorithmic_bytes": alg, "kernel": "bf16_fast_kernel<32> (one launch per step)"},
         "rotating_buffers": nrot,
     }
     if not args.no_cpu:

@@ -13,8 +13,8 @@
 
 namespace lmrs {
 
-constexpr int kThreads = 1024;  // one workgroup per row: 16 waves of 64
-constexpr int kWaves = kThreads / 64;
+constexpr int kThreads = 1024;  // workgroup of the generic engine: 16 waves of 64
+constexpr int kWaves = kThreads / 64;  // the most waves any workgroup here has
 
 // ---- bf16 <-> f32 ----------------------------------------------------------
 
@@ -159,30 +159,30 @@ template <class T>
 __device__ __forceinline__ T wave_min(T v) { return lane63(wave_inclusive<OpMin>(v, (T)~T(0))); }
 __device__ __forceinline__ int32_t wave_min(int32_t v) { return lane63(wave_inclusive<OpMin>(v, (int32_t)0x7FFFFFFF)); }
 
-// Block-wide reductions.  `scratch` holds kWaves elements of T; every
-// thread returns the (scalar) result.  Contains two barriers.
-template <class Op, class T>
+// Block-wide reductions over NW waves.  `scratch` holds NW elements of T;
+// every thread returns the (scalar) result.  Contains two barriers.
+template <int NW, class Op, class T>
 __device__ __forceinline__ T block_reduce(T w, T *scratch) {
   __syncthreads();
   if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = w;
   __syncthreads();
   T r = scratch[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) r = Op::apply(r, scratch[i]);
+  for (int i = 1; i < NW; ++i) r = Op::apply(r, scratch[i]);
   return uniform(r);
 }
 
-template <typename T>
-__device__ T block_sum(T v, T *scratch) { return block_reduce<OpSum>(wave_sum(v), scratch); }
-template <typename T>
-__device__ T block_max(T v, T *scratch) { return block_reduce<OpMax>(wave_max(v), scratch); }
-template <typename T>
-__device__ T block_min(T v, T *scratch) { return block_reduce<OpMin>(wave_min(v), scratch); }
+template <int NW = kWaves, typename T>
+__device__ __forceinline__ T block_sum(T v, T *scratch) { return block_reduce<NW, OpSum>(wave_sum(v), scratch); }
+template <int NW = kWaves, typename T>
+__device__ __forceinline__ T block_max(T v, T *scratch) { return block_reduce<NW, OpMax>(wave_max(v), scratch); }
+template <int NW = kWaves, typename T>
+__device__ __forceinline__ T block_min(T v, T *scratch) { return block_reduce<NW, OpMin>(wave_min(v), scratch); }
 
-// Exclusive prefix sum over the block in thread order.  Returns the
-// exclusive prefix of `v`; *total receives the block total.  Two barriers.
-template <typename T>
-__device__ T block_exclusive_scan(T v, T *scratch, T *total) {
+// Exclusive prefix sum over the block (NW waves) in thread order.  Returns
+// the exclusive prefix of `v`; *total receives the block total.  Two barriers.
+template <int NW = kWaves, typename T>
+__device__ __forceinline__ T block_exclusive_scan(T v, T *scratch, T *total) {
   const int wave = threadIdx.x >> 6;
   const T incl = wave_inclusive<OpSum>(v, T(0));
   const T wtot = lane63(incl);
@@ -191,7 +191,7 @@ __device__ T block_exclusive_scan(T v, T *scratch, T *total) {
   __syncthreads();
   T off = T(0), tot = T(0);
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) {
+  for (int i = 0; i < NW; ++i) {
     const T s = scratch[i];
     if (i < wave) off += s;
     tot += s;

@@ -1,11 +1,11 @@
 // generic_engine.hpp -- the general-purpose selection engine (any dtype, any
 // vocab up to LMRS_MAX_VOCAB, any parameters).
 //
-// One workgroup of 1024 threads owns one row.  A "row source" supplies, on
-// every pass, the total-order key of each processed element: StreamRow
-// re-reads the row from memory and re-applies the processor chain, RegRow
-// (fast_bf16.hpp) walks keys already held in registers.  Selection never
-// sorts the row: it runs radix selections on 32-bit keys with LDS histograms
+// One workgroup (of 1024 threads, or of the 512 threads of a fast kernel that
+// hands it a row) owns one row.  The row source, StreamRow, supplies on every
+// pass the total-order key of each processed element: it re-reads the row
+// from memory and re-applies the processor chain.  Selection never sorts the
+// row: it runs radix selections on 32-bit keys with LDS histograms
 // (counts for top-k, counts plus f64 weight sums for the nucleus cut and the
 // inverse-CDF draw) and resolves ties by lowest index with a radix selection
 // on the index.  Small top-k candidate sets are gathered into LDS, sorted
@@ -62,9 +62,10 @@ struct SelState {
 };
 
 // A row streamed from global memory; every pass re-reads and re-processes it.
-template <int DT>
+template <int DT, int NT_ = kThreads>
 struct StreamRow {
   using TR = DTypeTraits<DT>;
+  static constexpr int NT = NT_;
   const void *base;
   int64_t vocab;
   bool vec;  // 16-byte aligned rows use dwordx4 loads
@@ -82,7 +83,7 @@ struct StreamRow {
       if (vec) {
         const int64_t nch = vocab >> 3;
         const uint4 *p4 = (const uint4 *)p;
-        for (int64_t ch = threadIdx.x; ch < nch; ch += kThreads) {
+        for (int64_t ch = threadIdx.x; ch < nch; ch += NT) {
           uint4 d = p4[ch];
           uint32_t w[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
@@ -95,7 +96,7 @@ struct StreamRow {
         }
         done = nch << 3;
       }
-      for (int64_t i = done + threadIdx.x; i < vocab; i += kThreads) {
+      for (int64_t i = done + threadIdx.x; i < vocab; i += NT) {
         uint32_t y = process_bf16(p[i], (uint32_t)i, c, *ht);
         f((uint32_t)i, order_key(bf16_to_f32(y)) & 0xFFFF0000u);
       }
@@ -105,7 +106,7 @@ struct StreamRow {
       if (vec) {
         const int64_t nch = vocab >> 2;
         const float4 *p4 = (const float4 *)p;
-        for (int64_t ch = threadIdx.x; ch < nch; ch += kThreads) {
+        for (int64_t ch = threadIdx.x; ch < nch; ch += NT) {
           float4 d = p4[ch];
           float w[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
@@ -116,7 +117,7 @@ struct StreamRow {
         }
         done = nch << 2;
       }
-      for (int64_t i = done + threadIdx.x; i < vocab; i += kThreads)
+      for (int64_t i = done + threadIdx.x; i < vocab; i += NT)
         f((uint32_t)i, order_key(process_f32(p[i], (uint32_t)i, c, *ht)));
     }
   }
@@ -134,13 +135,14 @@ struct CountSel {
 template <class Row, class VF>
 __device__ __forceinline__ CountSel select_kth_largest(SelState &ss, const Row &row, VF vf, uint32_t k,
                                                        int total_bits, const int *widths, int nlev) {
+  constexpr int NT = Row::NT, NW = NT / 64, P = kBins / NT;
   uint32_t prefix = 0, krem = k, ngt = 0, neq = 0;
   int fixed = 0;
   for (int lev = 0; lev < nlev; ++lev) {
     const int w = widths[lev];
     const int shift = total_bits - fixed - w;
     const uint32_t nb = 1u << w;
-    for (uint32_t i = threadIdx.x; i < nb; i += kThreads) ss.bcnt[i] = 0u;
+    for (uint32_t i = threadIdx.x; i < nb; i += NT) ss.bcnt[i] = 0u;
     __syncthreads();
     row.for_each([&](uint32_t idx, uint32_t key) {
       uint32_t val;
@@ -149,21 +151,24 @@ __device__ __forceinline__ CountSel select_kth_largest(SelState &ss, const Row &
       atomicAdd(&ss.bcnt[(val >> shift) & (nb - 1u)], 1u);
     });
     __syncthreads();
-    // Bins in descending digit order: thread t owns digits nb-1-2t, nb-2-2t.
-    const int d0 = (int)nb - 1 - 2 * (int)threadIdx.x, d1 = d0 - 1;
-    const uint32_t c0 = d0 >= 0 ? ss.bcnt[d0] : 0u, c1 = d1 >= 0 ? ss.bcnt[d1] : 0u;
-    uint32_t tot;
-    const uint32_t above0 = block_exclusive_scan(c0 + c1, ss.uscr, &tot);
-    const uint32_t above1 = above0 + c0;
-    if (d0 >= 0 && c0 > 0 && above0 < krem && krem <= above0 + c0) {
-      ss.sel[0] = (uint32_t)d0;
-      ss.sel[1] = above0;
-      ss.sel[2] = c0;
+    // Bins in descending digit order: thread t owns digits nb-1-P*t-j, j < P.
+    uint32_t cj[P], sum = 0;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int d = (int)nb - 1 - P * (int)threadIdx.x - j;
+      cj[j] = d >= 0 ? ss.bcnt[d] : 0u;
+      sum += cj[j];
     }
-    if (d1 >= 0 && c1 > 0 && above1 < krem && krem <= above1 + c1) {
-      ss.sel[0] = (uint32_t)d1;
-      ss.sel[1] = above1;
-      ss.sel[2] = c1;
+    uint32_t tot;
+    uint32_t acc = block_exclusive_scan<NW>(sum, ss.uscr, &tot);
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      if (cj[j] > 0 && acc < krem && krem <= acc + cj[j]) {
+        ss.sel[0] = (uint32_t)((int)nb - 1 - P * (int)threadIdx.x - j);
+        ss.sel[1] = acc;
+        ss.sel[2] = cj[j];
+      }
+      acc += cj[j];
     }
     __syncthreads();
     const uint32_t d = uniform(ss.sel[0]), above = uniform(ss.sel[1]);
@@ -202,6 +207,7 @@ __device__ __forceinline__ WeightSel select_by_weight(SelState &ss, const Row &r
                                                       uint32_t clamp_key, uint32_t clamp_excess,
                                                       float M) {
   using TR = typename Row::TR;
+  constexpr int NT = Row::NT, NW = NT / 64, P = kBins / NT;
   uint32_t prefix = 0;
   int fixed = 0;
   double target = 0.0, above_acc = 0.0, total = 0.0;
@@ -212,7 +218,7 @@ __device__ __forceinline__ WeightSel select_by_weight(SelState &ss, const Row &r
     const int w = TR::kWidths[lev];
     const int shift = 32 - fixed - w;
     const uint32_t nb = 1u << w;
-    for (uint32_t i = threadIdx.x; i < nb; i += kThreads) {
+    for (uint32_t i = threadIdx.x; i < nb; i += NT) {
       ss.bcnt[i] = 0u;
       ss.bw[i] = 0.0;
     }
@@ -233,34 +239,48 @@ __device__ __forceinline__ WeightSel select_by_weight(SelState &ss, const Row &r
       ss.bw[d] -= (double)clamp_excess * (double)expf(TR::value(clamp_key) - M);
     }
     __syncthreads();
-    const int d0 = (int)nb - 1 - 2 * (int)threadIdx.x, d1 = d0 - 1;
-    const uint32_t c0 = d0 >= 0 ? ss.bcnt[d0] : 0u, c1 = d1 >= 0 ? ss.bcnt[d1] : 0u;
-    const double w0 = d0 >= 0 ? ss.bw[d0] : 0.0, w1 = d1 >= 0 ? ss.bw[d1] : 0.0;
+    // thread t owns digits nb-1-P*t-j (positions P*t+j in descending order)
+    uint32_t cj[P];
+    double wj[P], wsum = 0.0;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      const int d = (int)nb - 1 - P * (int)threadIdx.x - j;
+      cj[j] = d >= 0 ? ss.bcnt[d] : 0u;
+      wj[j] = d >= 0 ? ss.bw[d] : 0.0;
+      wsum += wj[j];
+    }
     double tot;
-    const double above0 = block_exclusive_scan(w0 + w1, ss.dscr, &tot);
-    const double above1 = above0 + w0;
+    const double above_t = block_exclusive_scan<NW>(wsum, ss.dscr, &tot);
     if (lev == 0) {
       total = tot;
       target = frac * tot;
     }
-    // First non-empty bin (descending) whose inclusive cumulative reaches the target.
-    int pos = 0x7FFFFFFF;
-    if (d0 >= 0 && c0 > 0 && above0 + w0 >= target) pos = 2 * (int)threadIdx.x;
-    else if (d1 >= 0 && c1 > 0 && above1 + w1 >= target) pos = 2 * (int)threadIdx.x + 1;
-    // Last non-empty bin, for the rounding fallback.
-    int last = -1;
-    if (d1 >= 0 && c1 > 0) last = 2 * (int)threadIdx.x + 1;
-    else if (d0 >= 0 && c0 > 0) last = 2 * (int)threadIdx.x;
-    pos = block_min(pos, ss.iscr);
-    last = block_max(last, ss.iscr);
+    // First non-empty bin (descending) whose inclusive cumulative reaches the
+    // target; last non-empty bin, for the rounding fallback.
+    int pos = 0x7FFFFFFF, last = -1;
+    double accw = above_t;
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+      if (cj[j] > 0 && pos == 0x7FFFFFFF && accw + wj[j] >= target) pos = P * (int)threadIdx.x + j;
+      if (cj[j] > 0) last = P * (int)threadIdx.x + j;
+      accw += wj[j];
+    }
+    pos = block_min<NW>(pos, ss.iscr);
+    last = block_max<NW>(last, ss.iscr);
     const bool ovf = pos == 0x7FFFFFFF;
     const int pick = ovf ? last : pos;
-    if ((int)threadIdx.x == pick / 2) {
-      const bool first = (pick & 1) == 0;
-      ss.sel[0] = (uint32_t)(first ? d0 : d1);
-      ss.sel[1] = first ? c0 : c1;
-      ss.dsel[0] = first ? above0 : above1;
-      ss.dsel[1] = first ? w0 : w1;
+    if ((int)threadIdx.x == pick / P) {
+      double accp = above_t;
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        if (P * (int)threadIdx.x + j == pick) {
+          ss.sel[0] = (uint32_t)((int)nb - 1 - pick);
+          ss.sel[1] = cj[j];
+          ss.dsel[0] = accp;
+          ss.dsel[1] = wj[j];
+        }
+        accp += wj[j];
+      }
     }
     __syncthreads();
     const uint32_t d = uniform(ss.sel[0]);
@@ -299,14 +319,15 @@ __device__ __forceinline__ void write_row(const lmrs_sample_args &a, int r, uint
 }
 
 // Sorts ss.gather[0..n) ascending (bitonic; n <= kGatherCap).  Barriers inside.
+template <int NT = kThreads>
 __device__ __forceinline__ void sort_gather(SelState &ss, uint32_t n) {
   uint32_t n2 = 1;
   while (n2 < n) n2 <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < n2; i += kThreads) ss.gather[i] = ~0ull;
+  for (uint32_t i = n + threadIdx.x; i < n2; i += NT) ss.gather[i] = ~0ull;
   __syncthreads();
   for (uint32_t kk = 2; kk <= n2; kk <<= 1) {
     for (uint32_t jj = kk >> 1; jj > 0; jj >>= 1) {
-      for (uint32_t i = threadIdx.x; i < n2; i += kThreads) {
+      for (uint32_t i = threadIdx.x; i < n2; i += NT) {
         const uint32_t ixj = i ^ jj;
         if (ixj > i) {
           const uint64_t x = ss.gather[i], y = ss.gather[ixj];
@@ -327,15 +348,16 @@ __device__ __forceinline__ void sort_gather(SelState &ss, uint32_t n) {
 // order.  Applies the nucleus cut (top_p.rs:45-58) and softmax_choice
 // (strategies/mod.rs:27-55) with f64 weights exp(f64(l - max)) and f64
 // prefix sums, and writes the outputs.
-template <class TR>
+template <class TR, int NT = kThreads>
 __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, const lmrs_sample_args &a,
                                               int r, uint32_t k) {
-  // Thread t owns sorted entries 4t .. 4t+3 of the first k.
+  // Thread t owns sorted entries P*t .. P*t+P-1 of the first k.
+  constexpr int P = kGatherCap / NT, NW = NT / 64;
   const float M = TR::value(~uniform((uint32_t)(ss.gather[0] >> 32)));
-  double wv[4], incl[4], local = 0.0;
+  double wv[P], incl[P], local = 0.0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
+  for (int q = 0; q < P; ++q) {
+    const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
     wv[q] = 0.0;
     if (i < k) {
       const float y = TR::value(~(uint32_t)(ss.gather[i] >> 32));
@@ -345,9 +367,9 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
     incl[q] = local;
   }
   double sum_all;
-  const double excl = block_exclusive_scan(local, ss.dscr, &sum_all);
+  const double excl = block_exclusive_scan<NW>(local, ss.dscr, &sum_all);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) incl[q] += excl;
+  for (int q = 0; q < P; ++q) incl[q] += excl;
   if (!(__builtin_isfinite(sum_all) && sum_all > 0.0)) {
     if (threadIdx.x == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
     return;
@@ -357,16 +379,16 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
   if (c.top_p < 1.0) {
     int first = 0x7FFFFFFF;
 #pragma unroll
-    for (int q = 3; q >= 0; --q) {
-      const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
+    for (int q = P - 1; q >= 0; --q) {
+      const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
       if (i < k && incl[q] / sum_all >= c.top_p) first = (int)i;
     }
-    first = block_min(first, ss.iscr);
+    first = block_min<NW>(first, ss.iscr);
     if (first != 0x7FFFFFFF) keep = (uint32_t)first + 1u;
     // nucleus margin at the cut
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
+    for (int q = 0; q < P; ++q) {
+      const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
       if (i + 1u == keep) {
         const double acc = incl[q] / sum_all, prev = (incl[q] - wv[q]) / sum_all;
         double m = c.top_p - prev;
@@ -380,22 +402,22 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
   }
   // sum over the kept prefix, held by the owner of entry keep-1
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
-    if (4u * threadIdx.x + (uint32_t)q + 1u == keep) ss.dsel[3] = incl[q];
+  for (int q = 0; q < P; ++q)
+    if ((uint32_t)P * threadIdx.x + (uint32_t)q + 1u == keep) ss.dsel[3] = incl[q];
   __syncthreads();
   const double sum_keep = uniform(ss.dsel[3]);
   const double target = c.u * sum_keep;
   int pick = 0x7FFFFFFF;
 #pragma unroll
-  for (int q = 3; q >= 0; --q) {
-    const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
+  for (int q = P - 1; q >= 0; --q) {
+    const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
     if (i < keep && target <= incl[q]) pick = (int)i;
   }
-  pick = block_min(pick, ss.iscr);
+  pick = block_min<NW>(pick, ss.iscr);
   if (pick == 0x7FFFFFFF) pick = (int)keep - 1;  // fallback: last candidate (mod.rs:52-54)
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint32_t i = 4u * threadIdx.x + (uint32_t)q;
+  for (int q = 0; q < P; ++q) {
+    const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
     if ((int)i == pick) {
       const uint64_t g = ss.gather[i];
       const uint32_t token = (uint32_t)(g & 0xFFFFFFFFu);
@@ -424,8 +446,8 @@ __device__ __forceinline__ void finish_small_k(SelState &ss, const Row &row, con
     ss.gather[s] = ((uint64_t)(~key) << 32) | (uint64_t)idx;
   });
   __syncthreads();
-  sort_gather(ss, n);
-  finish_sorted<typename Row::TR>(ss, c, a, r, k);
+  sort_gather<Row::NT>(ss, n);
+  finish_sorted<typename Row::TR, Row::NT>(ss, c, a, r, k);
 }
 
 // The whole selection for one row from any row source: greedy, top-k,
@@ -530,8 +552,8 @@ __device__ __forceinline__ void row_stats(SelState &ss, const Row &row, uint32_t
     best = pk > best ? pk : best;
     neg += key < TR::kNegInfKey ? 1u : 0u;
   });
-  best = block_max(best, ss.qscr);
-  nneg = block_sum(neg, ss.uscr);
+  best = block_max<Row::NT / 64>(best, ss.qscr);
+  nneg = block_sum<Row::NT / 64>(neg, ss.uscr);
   kmax = (uint32_t)(best >> 32);
   imax = ~(uint32_t)(best & 0xFFFFFFFFu);
 }
@@ -542,11 +564,8 @@ struct GenericShared {
   RowCfg cfg;
 };
 
-// Token id the fast kernels write for rows they leave to the generic pass.
-constexpr uint32_t kDeferred = 0xFFFFFFFFu;
-
-// One row through the generic engine (all threads of the workgroup).
-template <int DT>
+// One row through the generic engine (all NT threads of the workgroup).
+template <int DT, int NT = kThreads>
 __device__ __forceinline__ void generic_row(GenericShared &sh, const lmrs_sample_args &a, int r, int vec) {
   using TR = DTypeTraits<DT>;
   if (threadIdx.x == 0) sh.cfg = load_row_cfg(a, r, DT);
@@ -558,8 +577,8 @@ __device__ __forceinline__ void generic_row(GenericShared &sh, const lmrs_sample
       write_row(a, r, 0u, 0.0f, 0.0f, c.status != LMRS_ROW_OK ? c.status : LMRS_ROW_EMPTY);
     return;
   }
-  if (c.hist_on) build_history(sh.ht, a, c, V);
-  StreamRow<DT> row;
+  if (c.hist_on) build_history<NT>(sh.ht, a, c, V);
+  StreamRow<DT, NT> row;
   row.base = (const char *)a.logits + (size_t)r * (size_t)a.row_stride * TR::kElemBytes;
   row.vocab = V;
   row.vec = vec != 0;
@@ -574,19 +593,6 @@ template <int DT>
 __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_args a, int vec) {
   __shared__ GenericShared sh;
   generic_row<DT>(sh, a, blockIdx.x, vec);
-}
-
-// Finishes the rows a fast kernel marked kDeferred (launched right after it
-// on the same stream); a few workgroups stride over the batch.
-template <int DT>
-__global__ void __launch_bounds__(kThreads) generic_deferred_kernel(lmrs_sample_args a, int vec) {
-  __shared__ GenericShared sh;
-  for (int r = blockIdx.x; r < a.batch; r += gridDim.x) {
-    if (a.token_ids[r] != kDeferred) continue;  // same address for every thread: uniform
-    __syncthreads();
-    generic_row<DT>(sh, a, r, vec);
-    __syncthreads();
-  }
 }
 
 // LogitsProcessor::process for the three reference processors, batched.

@@ -124,17 +124,18 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   return c;
 }
 
-// Builds the history tables for the row (all threads; ends with a barrier).
+// Builds the history tables for the row (all NT threads; ends with a barrier).
+template <int NT = kThreads>
 __device__ inline void build_history(HistoryTables &ht, const lmrs_sample_args &a,
                                      const RowCfg &c, int64_t vocab) {
-  for (int i = threadIdx.x; i < kHashCap; i += kThreads) {
+  for (int i = threadIdx.x; i < kHashCap; i += NT) {
     ht.keys[i] = 0u;
     ht.counts[i] = 0u;
   }
   const int words = (int)((vocab + 31) >> 5);
-  for (int i = threadIdx.x; i < words; i += kThreads) ht.bitmap[i] = 0u;
+  for (int i = threadIdx.x; i < words; i += NT) ht.bitmap[i] = 0u;
   __syncthreads();
-  for (int64_t j = threadIdx.x; j < c.h_len; j += kThreads) {
+  for (int64_t j = threadIdx.x; j < c.h_len; j += NT) {
     uint32_t t = a.hist_ids[c.h_begin + j];
     if ((int64_t)t >= vocab) continue;  // ids outside the vocab are ignored
     atomicOr(&ht.bitmap[t >> 5], 1u << (t & 31u));

@@ -8,9 +8,6 @@
 
 namespace {
 
-// Workgroups of the pass that finishes deferred rows.
-constexpr int kDeferredGrid = 64;
-
 int check_args(const lmrs_sample_args *a, bool need_tokens) {
   if (!a) return LMRS_ERR_NULL_ARGUMENT;
   if (a->dtype != LMRS_DTYPE_BF16 && a->dtype != LMRS_DTYPE_F32) return LMRS_ERR_BAD_DTYPE;
@@ -39,19 +36,18 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
   const int vec = vector_ok(args);
   const int64_t V = args->vocab;
   if (args->dtype == LMRS_DTYPE_BF16 && vec && V > 0 && V % 8 == 0 && V <= lmrs::kFastMaxVocab) {
-    // register-resident rows: NCH chunks of 8 logits per thread, then the
-    // generic pass for the rows the fast kernel deferred
-    const dim3 grid(args->batch), block(lmrs::kThreads);
-    if (V <= 4 * 8192)
-      lmrs::bf16_fast_kernel<4><<<grid, block, 0, s>>>(*args);
-    else if (V <= 8 * 8192)
+    // register-resident rows: NCH chunks of 8 logits per thread (rows the
+    // fast path does not take finish in the generic engine, in the same launch)
+    const dim3 grid(args->batch), block(lmrs::kFT);
+    constexpr int kRowsPerSlot = 8 * lmrs::kRT;  // logits per chunk slot of the row threads
+    if (V <= 8 * kRowsPerSlot)
       lmrs::bf16_fast_kernel<8><<<grid, block, 0, s>>>(*args);
-    else if (V <= 16 * 8192)
+    else if (V <= 16 * kRowsPerSlot)
       lmrs::bf16_fast_kernel<16><<<grid, block, 0, s>>>(*args);
+    else if (V <= 32 * kRowsPerSlot)
+      lmrs::bf16_fast_kernel<32><<<grid, block, 0, s>>>(*args);
     else
-      lmrs::bf16_fast_kernel<20><<<grid, block, 0, s>>>(*args);
-    const int g2 = args->batch < kDeferredGrid ? args->batch : kDeferredGrid;
-    lmrs::generic_deferred_kernel<LMRS_DTYPE_BF16><<<g2, lmrs::kThreads, 0, s>>>(*args, vec);
+      lmrs::bf16_fast_kernel<lmrs::kMaxSlots><<<grid, block, 0, s>>>(*args);
   } else if (args->dtype == LMRS_DTYPE_BF16)
     lmrs::generic_sample_kernel<LMRS_DTYPE_BF16><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
   else
