@@ -95,6 +95,9 @@ struct OpMax {
 struct OpMin {
   template <class T> __device__ static T apply(T a, T b) { return a < b ? a : b; }
 };
+struct OpOr {
+  template <class T> __device__ static T apply(T a, T b) { return a | b; }
+};
 
 template <class T>
 struct Bits;

@@ -1,41 +1,38 @@
 // fast_bf16.hpp -- the bf16 sampling kernel for rows of up to kFastMaxVocab.
 //
 // One workgroup of 512 threads (one per CU at this LDS size; 8 waves, so each
-// thread may hold 256 VGPRs) owns one row.  Its waves are specialised: wave 0
-// handles the history (below) while waves 1..7, the row threads, stream the
-// row.  Each row thread loads its NCH 16-byte chunks (chunk c = s * 448 + row
-// thread) in one burst at kernel entry and converts them to 16-bit
-// total-order keys of the RAW logits;
-// that single pass over registers also records, in LDS, the largest
-// non-history key of every chunk (the "chunk maxima", 2 bytes per 8 logits).
-// After it the row's registers are dead on the top-k and greedy paths: every
-// later step is a short loop over LDS data (chunk maxima, the history
-// members, candidate lists) plus a re-read of the few chunks whose maximum
-// can hold a candidate.  Keeping the code after the load pass small matters
-// as much as its arithmetic: each row executes it once, so its instructions
-// are fetched cold.
+// thread may hold 256 VGPRs) owns one row.  Each thread loads its NCH 16-byte
+// chunks (chunk c = s * 512 + thread, slot s = 0 .. NCH-1) with explicitly
+// issued loads and keeps them in registers as 16-bit total-order keys of the
+// RAW logits, two per word: the row is read from memory once.
 //
-// Penalties never touch the per-element pass.  The history wave loads the
-// history ids, finds the distinct tokens ("members", at most kFastMembers)
-// with an LDS hash, fetches their raw logits with one load each and computes
-// their penalised keys z (Repetition then Presence/Frequency, bf16-rounded
-// per op, as the reference's chain of kernels), all while the row streams in.  Chunk maxima
-// skip members; members take part in every selection through their z keys.
+// History.  The history ids are loaded first.  While the first part of the
+// row streams in, they are marked in an LDS bitmap over the vocab; a rank map
+// (per 32-token word: the number of history tokens before it, and the word)
+// then gives every distinct history token ("member", at most kFastMembers) a
+// dense index in token order, under which its multiplicity is counted.  The
+// load pass meets every member in registers and stores its raw key under its
+// index, so penalties need no gather from memory.  Each member's penalised
+// key z (Repetition then Presence/Frequency, bf16-rounded per op, as the
+// reference's chain of kernels) is computed once from its raw key and count.
 // Temperature is not applied per element either: y = bf16(fma(z, 1/T, 0)) is
 // monotone in z, so selection runs on z keys and maps only the keys that
 // matter to y; runs of z keys that round to one y form one tie group, whose
 // tokens are ordered by index as the reference's sort orders them.
 //
 // Paths after the load pass:
-//   greedy   (top_k == 1): the largest z is the largest chunk maximum or
-//            member key; the lowest index of its tie group comes from the
-//            chunks whose maximum reaches the group.
-//   small k  (top_k <= kGatherCap): the k-th largest value among chunk maxima
-//            and member keys, L, bounds the k-th largest z from below (each
-//            value is a distinct element).  Every element with z at or above
-//            the start of L's tie group is gathered (re-reading the chunks
-//            whose maximum reaches it), sorted exactly -- inside one wave
-//            when there are at most 64 -- and finished in f64.
+//   small k  (top_k <= kSmallK, greedy included): every thread holds one
+//            "thread value", the largest key of its chunks without members,
+//            raised to its members' z keys.  The K-th largest thread value L
+//            (a 256-bin LDS histogram) bounds the K-th largest z from below,
+//            each value being a distinct element.  The chunks whose maximum
+//            reaches the start of L's tie group are copied to LDS, their
+//            elements (and members) at or above it become the candidates,
+//            which one wave sorts and finishes in f64 when there are at most
+//            64 of them.
+//   mid k    (top_k <= kGatherCap): the same bound from the K-th largest
+//            chunk maximum (a cascade of LDS windows), the candidates
+//            gathered from registers and sorted in LDS.
 //   full     (otherwise): a 65536-bin count histogram of the keys in
 //            registers (two 16-bit counters per LDS word), compacted to its
 //            non-empty keys; per-key weights exp(f64(y - max)) times counts
@@ -54,16 +51,19 @@ namespace lmrs {
 
 constexpr int kFT = 512;            // threads of a fast-kernel workgroup
 constexpr int kFW = kFT / 64;       // its waves
-constexpr int kHW = 0;              // leading waves that hold no row data
-constexpr int kRT = kFT - 64 * kHW; // row threads
-constexpr int kRW = kRT / 64;       // row waves
 constexpr int kMaxEntries = 6144;   // distinct keys the full path keeps in LDS
 constexpr int kFastMembers = 2048;  // distinct history tokens the fast path keeps
-constexpr int kMaxSlots = 40;       // chunk slots per row thread
-constexpr int kFastMaxVocab = kMaxSlots * 8 * kRT;
+constexpr int kMaxSlots = 40;       // chunk slots per thread
+constexpr int kFastMaxVocab = kMaxSlots * 8 * kFT;
+constexpr int kMaxWords = kFastMaxVocab / 32;  // bitmap words
+constexpr int kWordsPer = kMaxWords / kFT;     // bitmap words per thread (rank map build)
 constexpr int kMaxWindow = kFT;     // widest window of the count cascade (one bin per thread)
 constexpr int kHistPer = LMRS_MAX_HISTORY / kFT;
 constexpr int kMemPer = kFastMembers / kFT;
+constexpr int kSmallK = 64;         // top_k bound of the thread-value path
+constexpr int kTvBins = 256;        // bins of the thread-value histogram
+constexpr int kDumpCap = 1024;      // chunks the thread-value path copies to LDS
+
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -224,37 +224,69 @@ __device__ __forceinline__ uint32_t penalise_member(uint32_t raw, uint32_t count
 //   full path: [0, 128K) 65536 16-bit counters; after compaction [128K, 152K)
 //   the entries (key << 16 | count) and [0, 72K) their prefixes; for the
 //   final search the member list is rebuilt and [128K, 134K) holds the
-//   per-slot / per-thread counts of the ordered search
+// LDS arena with phase-dependent views (byte offsets):
+//   [0, 40K)      chunk maxima of the load pass (then SelState)
+//   [0, 57K)      SelState: candidate list, sort and finish scratch
+//   [60K, 62K)    window histogram (thread values; count cascade)
+//   [62K, 62K+64) counters of the small-k path
+//   [64K, 84K)    membership bitmap over the vocab (history build); then the
+//                 chunks copied by the small-k path: keys [64K, 80K),
+//                 chunk index | member bits << 24 [80K, 84K)
+//   [84K, 124K)   rank map: per bitmap word, (members before it, the word)
+//                 (history build); then the member bits of the load pass
+//   [128K, 152K)  members: token ids, multiplicities, raw key | z key << 16
+//   full path: [0, 128K) 65536 16-bit counters; after compaction [128K, 152K)
+//   the entries (key << 16 | count) -- the member list waits in registers
+//   meanwhile -- and [0, 72K) their prefixes; the ordered search keeps its
+//   per-slot / per-thread counts at [0, 4K)
 constexpr int kArenaBytes = 152 * 1024;
-constexpr int kOffBitmap = 64 * 1024;
 constexpr int kOffWhist = 60 * 1024;
-constexpr int kOffSlotCnt = 128 * 1024;
-constexpr int kOffTcnt = kOffSlotCnt + kMaxSlots * kRW * 4;
-constexpr int kOffMembers = 136 * 1024;
+constexpr int kOffCounters = 62 * 1024;
+constexpr int kOffBitmap = 64 * 1024;
+constexpr int kOffDumpKeys = 64 * 1024;
+constexpr int kOffDumpMeta = 80 * 1024;
+constexpr int kOffRankMap = 84 * 1024;
+constexpr int kOffMembers = 128 * 1024;
 constexpr int kOffEntries = 128 * 1024;
-static_assert((int)sizeof(SelState) <= kOffBitmap, "SelState view");
-static_assert(kOffBitmap + (kFastMaxVocab + 31) / 32 * 4 <= kOffSlotCnt, "bitmap view");
-static_assert((int)sizeof(SelState) <= kOffWhist && kOffWhist + kMaxWindow * 4 <= kOffBitmap, "window view");
-static_assert(kOffTcnt + kRT * 4 <= kOffMembers, "count views");
-static_assert(kOffMembers + kFastMembers * 8 <= kArenaBytes, "member view");
+constexpr int kOffCm = 0;
+constexpr int kOffHb = kOffRankMap;
+constexpr int kOffSlotCnt = 0;
+constexpr int kOffTcnt = kMaxSlots * kFW * 4;
+static_assert((int)sizeof(SelState) <= kOffWhist, "SelState view");
+static_assert(kOffWhist + kMaxWindow * 4 <= kOffCounters && kTvBins <= kMaxWindow, "window view");
+static_assert(kOffCounters + 64 <= kOffBitmap, "counter view");
+static_assert(kOffBitmap + kMaxWords * 4 <= kOffRankMap, "bitmap view");
+static_assert(kOffDumpKeys + kDumpCap * 16 <= kOffDumpMeta && kOffDumpMeta + kDumpCap * 4 <= kOffRankMap,
+              "chunk copy view");
+static_assert(kOffRankMap + kMaxWords * 8 <= kOffMembers, "rank map view");
+static_assert(kOffCm + kMaxSlots / 2 * kFT * 4 <= kOffWhist, "chunk maxima view");
+static_assert(kOffHb + kMaxSlots / 4 * kFT * 4 <= kOffMembers, "member bits view");
+static_assert(kOffMembers + kFastMembers * 12 <= kArenaBytes, "member view");
 static_assert(kOffEntries + kMaxEntries * 4 <= kArenaBytes, "entries view");
 static_assert(kMaxEntries * 12 <= kOffEntries, "prefix view");
-static_assert(kFastMembers % kFT == 0 && LMRS_MAX_HISTORY % kFT == 0, "per-thread counts");
+static_assert(kOffTcnt + kFT * 4 <= kOffEntries, "ordered search view");
+static_assert(kFastMembers % kFT == 0 && LMRS_MAX_HISTORY % kFT == 0 && kMaxWords % kFT == 0, "per-thread counts");
 
 struct FastShared {
   alignas(16) unsigned char arena[kArenaBytes];
   double dscr[kWaves];
   uint32_t uscr[kWaves];
   uint32_t uscr2[kWaves];
+  uint32_t uscr3[kWaves];
   int32_t iscr[kWaves];
   uint32_t chunk_z[8];
   uint32_t bsel[8];
 
   __device__ uint32_t *u32(int off) { return (uint32_t *)(arena + off); }
   __device__ uint32_t *m_idx() { return u32(kOffMembers); }
-  __device__ uint32_t *m_key() { return u32(kOffMembers + kFastMembers * 4); }
+  __device__ uint32_t *m_cnt() { return u32(kOffMembers + kFastMembers * 4); }
+  __device__ uint32_t *m_key() { return u32(kOffMembers + kFastMembers * 8); }
   __device__ uint32_t *bitmap() { return u32(kOffBitmap); }
+  __device__ uint2 *rank_map() { return (uint2 *)(arena + kOffRankMap); }
   __device__ uint32_t *whist() { return u32(kOffWhist); }
+  __device__ uint32_t *counters() { return u32(kOffCounters); }
+  __device__ uint4 *dump_keys() { return (uint4 *)(arena + kOffDumpKeys); }
+  __device__ uint32_t *dump_meta() { return u32(kOffDumpMeta); }
   __device__ SelState &ss() { return *(SelState *)(arena); }
 };
 
@@ -264,120 +296,58 @@ union FastOrGeneric {
   GenericShared g;
 };
 
-__device__ __forceinline__ bool member_bit(const uint32_t *bitmap, uint32_t i) {
-  return (bitmap[i >> 5] >> (i & 31u)) & 1u;
-}
-
-// Two block-wide maxima with one pair of barriers.
-__device__ __forceinline__ void block_max2(uint32_t &a, uint32_t &b, FastShared &sh) {
+// Three block-wide maxima with one pair of barriers.
+__device__ __forceinline__ void block_max3(uint32_t &a, uint32_t &b, uint32_t &c, FastShared &sh) {
   a = wave_max(a);
   b = wave_max(b);
+  c = wave_max(c);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) {
     sh.uscr[threadIdx.x >> 6] = a;
     sh.uscr2[threadIdx.x >> 6] = b;
+    sh.uscr3[threadIdx.x >> 6] = c;
   }
   __syncthreads();
-  uint32_t ra = sh.uscr[0], rb = sh.uscr2[0];
+  uint32_t ra = sh.uscr[0], rb = sh.uscr2[0], rc = sh.uscr3[0];
 #pragma unroll
   for (int i = 1; i < kFW; ++i) {
     ra = max(ra, sh.uscr[i]);
     rb = max(rb, sh.uscr2[i]);
+    rc = max(rc, sh.uscr3[i]);
   }
   a = uniform(ra);
   b = uniform(rb);
+  c = uniform(rc);
+}
+
+// Calls f(Index<s>) for a runtime value s in [B, E) that is uniform across
+// the wave, through a tree of scalar branches.
+template <int B, int E, class F>
+__device__ __forceinline__ void dispatch(int s, F &&f) {
+  if constexpr (E - B == 1) {
+    f(Index<B>{});
+  } else {
+    constexpr int M = (B + E) / 2;
+    if (s < M)
+      dispatch<B, M>(s, f);
+    else
+      dispatch<M, E>(s, f);
+  }
+}
+
+// Exclusive position of this lane's n items in a list, with one LDS atomic
+// per wave on *counter (which must start at zero for the list).
+__device__ __forceinline__ uint32_t wave_reserve(uint32_t n, uint32_t *counter) {
+  const uint32_t incl = wave_inclusive<OpSum>(n, 0u);
+  uint32_t base = 0u;
+  if ((threadIdx.x & 63) == 63 && incl) base = atomicAdd(counter, incl);
+  return (uint32_t)__builtin_amdgcn_readlane((int)base, 63) + incl - n;
 }
 
 // ---- history members ------------------------------------------------------------
 
-// History tables of the row in LDS: hash (token + 1 -> multiplicity) and the
-// membership bitmap; `hid` holds this thread's history ids (strided by the
-// block; entries at or past h_len are ignored).  Ends with a barrier.
-__device__ __forceinline__ void insert_history(FastShared &sh, const uint32_t (&hid)[kHistPer], int64_t h_len,
-                                               int64_t V) {
-  uint32_t *hkeys = sh.u32(0), *hcnt = sh.u32(kHashCap * 4), *bitmap = sh.bitmap();
-  // First probes of all this thread's ids together (independent atomics in
-  // flight at once); the few that collide continue probing afterwards.
-  uint32_t sl[kHistPer], prev[kHistPer];
-  bool live[kHistPer];
-#pragma unroll
-  for (int q = 0; q < kHistPer; ++q) {
-    const uint32_t t = hid[q];
-    live[q] = (int64_t)threadIdx.x + (int64_t)q * kFT < h_len && (int64_t)t < V;
-    sl[q] = hash_slot(t);
-    prev[q] = 0u;
-    if (live[q]) {
-      atomicOr(&bitmap[t >> 5], 1u << (t & 31u));
-      prev[q] = atomicCAS(&hkeys[sl[q]], 0u, t + 1u);
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < kHistPer; ++q) {
-    if (live[q]) {
-      const uint32_t t = hid[q];
-      uint32_t p = prev[q], s2 = sl[q];
-      while (p != 0u && p != t + 1u) {  // terminates: the table is at most half full
-        s2 = (s2 + 1u) & (kHashCap - 1);
-        p = atomicCAS(&hkeys[s2], 0u, t + 1u);
-      }
-      atomicAdd(&hcnt[s2], 1u);
-    }
-  }
-  __syncthreads();
-}
-
-// Clears the hash and the bitmap.  Ends with a barrier.
-__device__ __forceinline__ void clear_history(FastShared &sh) {
-  uint4 *p = (uint4 *)sh.u32(0);
-  constexpr int kVec = (kOffBitmap + kFastMaxVocab / 8) / 16;
-  for (int i = threadIdx.x; i < kVec; i += kFT) p[i] = make_uint4(0u, 0u, 0u, 0u);
-  __syncthreads();
-}
-
-// Compacts the hash into the member list (token ids; multiplicities in
-// m_key until the keys replace them).  Returns the member count (uniform).
-// Ends with a barrier.
-__device__ __forceinline__ uint32_t compact_members(FastShared &sh) {
-  const int tid = threadIdx.x;
-  constexpr int kPer = kHashCap / kFT;
-  const uint32_t *hkeys = sh.u32(0), *hcnt = sh.u32(kHashCap * 4);
-  uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
-  // thread t owns slots t, t + kFT, ...: conflict-free reads, all in flight at once
-  uint32_t keys[kPer];
-  uint32_t n = 0, nmem;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    keys[i] = hkeys[tid + i * kFT];
-    n += keys[i] ? 1u : 0u;
-  }
-  const uint32_t off = block_exclusive_scan<kFW>(n, sh.uscr, &nmem);
-  if (nmem <= (uint32_t)kFastMembers) {
-    uint32_t o = off;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      if (keys[i]) {
-        midx[o] = keys[i] - 1u;
-        mkey[o] = hcnt[tid + i * kFT];
-        ++o;
-      }
-    }
-  }
-  __syncthreads();
-  return nmem;
-}
-
-// This thread's history ids (strided by the block; positions past the end
-// re-read the first id and are ignored by insert_history).
-__device__ __forceinline__ void load_history_ids(uint32_t (&hid)[kHistPer], const lmrs_sample_args &a,
-                                                 const RowCfg &c) {
-#pragma unroll
-  for (int q = 0; q < kHistPer; ++q) {
-    const int64_t j = (int64_t)threadIdx.x + (int64_t)q * kFT;
-    hid[q] = a.hist_ids[c.h_begin + (j < c.h_len ? j : 0)];
-  }
-}
-
-// The same loads, issued (not waited for) as explicit instructions.
+// This thread's history ids (strided by the block), issued as explicit loads;
+// positions past the end re-read the first id and are ignored later.
 __device__ __forceinline__ void issue_history_ids(uint32_t (&hid)[kHistPer], const lmrs_sample_args &a,
                                                   const RowCfg &c) {
 #pragma unroll
@@ -387,18 +357,89 @@ __device__ __forceinline__ void issue_history_ids(uint32_t (&hid)[kHistPer], con
   }
 }
 
-// Raw logits of the members (one load each, a fixed number per thread).
-__device__ __forceinline__ void load_member_raw(uint32_t (&mraw)[kMemPer], FastShared &sh, uint32_t nmem,
-                                                const uint16_t *rowp) {
-  const uint32_t *midx = sh.m_idx();
-#pragma unroll
-  for (int q = 0; q < kMemPer; ++q) {
-    const uint32_t m = (uint32_t)threadIdx.x + (uint32_t)q * kFT;
-    mraw[q] = rowp[m < nmem ? midx[m] : 0u];
+__device__ __forceinline__ bool history_live(int q, uint32_t t, int64_t h_len, int64_t V) {
+  return (int64_t)threadIdx.x + (int64_t)q * kFT < h_len && (int64_t)t < V;
+}
+
+// Zeroes the small-k counters and histogram bins and, with a history, the
+// bitmap words and the multiplicities.  No barrier.
+__device__ __forceinline__ void clear_tables(FastShared &sh, bool hist, int nwords) {
+  const int tid = threadIdx.x;
+  if (tid < 16) sh.counters()[tid] = 0u;
+  if (tid < kTvBins) sh.whist()[tid] = 0u;
+  if (hist) {
+    uint4 *bm = (uint4 *)sh.bitmap();
+    for (int i = tid; i < (nwords + 3) / 4; i += kFT) bm[i] = make_uint4(0u, 0u, 0u, 0u);
+    uint4 *cnt = (uint4 *)sh.m_cnt();
+    for (int i = tid; i < kFastMembers / 4; i += kFT) cnt[i] = make_uint4(0u, 0u, 0u, 0u);
   }
 }
 
-// The same loads, issued (not waited for) as explicit instructions.
+// Marks the history ids below V in the bitmap.  Ends with a barrier.
+__device__ __forceinline__ void mark_history(FastShared &sh, const uint32_t (&hid)[kHistPer], int64_t h_len,
+                                             int64_t V) {
+  uint32_t *bm = sh.bitmap();
+#pragma unroll
+  for (int q = 0; q < kHistPer; ++q) {
+    const uint32_t t = hid[q];
+    if (history_live(q, t, h_len, V)) atomicOr(&bm[t >> 5], 1u << (t & 31u));
+  }
+  __syncthreads();
+}
+
+// The rank map: for bitmap word w, (the number of members with a token below
+// 32 w, the word).  Thread t owns words kWordsPer * t ... kWordsPer * t +
+// kWordsPer - 1, so one block scan orders them.  Returns the member count
+// (uniform).  Ends with a barrier.
+__device__ __forceinline__ uint32_t rank_members(FastShared &sh, int nwords) {
+  const int tid = threadIdx.x;
+  const uint32_t *bm = sh.bitmap();
+  uint2 *rm = sh.rank_map();
+  uint32_t w[kWordsPer];
+  uint32_t n = 0u;
+#pragma unroll
+  for (int i = 0; i < kWordsPer; ++i) {
+    const int j = tid * kWordsPer + i;
+    w[i] = j < nwords ? bm[j] : 0u;
+    n += (uint32_t)__builtin_popcount(w[i]);
+  }
+  uint32_t total;
+  uint32_t p = block_exclusive_scan<kFW>(n, sh.uscr, &total);
+#pragma unroll
+  for (int i = 0; i < kWordsPer; ++i) {
+    const int j = tid * kWordsPer + i;
+    if (j < nwords) rm[j] = make_uint2(p, w[i]);
+    p += (uint32_t)__builtin_popcount(w[i]);
+  }
+  __syncthreads();
+  return total;
+}
+
+// Index of member t (a marked token) in token order.
+__device__ __forceinline__ uint32_t member_rank(const uint2 &e, uint32_t bit) {
+  return e.x + (uint32_t)__builtin_popcount(e.y & ((1u << bit) - 1u));
+}
+
+// Token ids and multiplicities of the members, at their indices.  Ends with
+// a barrier.
+__device__ __forceinline__ void count_members(FastShared &sh, const uint32_t (&hid)[kHistPer], int64_t h_len,
+                                              int64_t V) {
+  const uint2 *rm = sh.rank_map();
+  uint32_t *cnt = sh.m_cnt(), *midx = sh.m_idx();
+#pragma unroll
+  for (int q = 0; q < kHistPer; ++q) {
+    const uint32_t t = hid[q];
+    if (history_live(q, t, h_len, V)) {
+      const uint32_t m = member_rank(rm[t >> 5], t & 31u);
+      atomicAdd(&cnt[m], 1u);
+      midx[m] = t;  // every copy of a token writes the same id
+    }
+  }
+  __syncthreads();
+}
+
+// Raw logits of the members, one 16-bit load each, issued (not waited for)
+// as explicit instructions.
 __device__ __forceinline__ void issue_member_raw(uint32_t (&mraw)[kMemPer], FastShared &sh, uint32_t nmem,
                                                  const uint16_t *rowp) {
   const uint32_t *midx = sh.m_idx();
@@ -414,12 +455,13 @@ __device__ __forceinline__ void issue_member_raw(uint32_t (&mraw)[kMemPer], Fast
 __device__ __forceinline__ uint32_t member_keys(FastShared &sh, const uint32_t (&mraw)[kMemPer], uint32_t nmem,
                                                 const RowCfg &c, uint32_t *bad) {
   uint32_t *mkey = sh.m_key();
+  const uint32_t *cnt = sh.m_cnt();
   uint32_t zmax = 0u;
 #pragma unroll
   for (int q = 0; q < kMemPer; ++q) {
     const uint32_t m = (uint32_t)threadIdx.x + (uint32_t)q * kFT;
     if (m < nmem) {
-      const uint32_t zk = bits_key16(penalise_member(mraw[q], mkey[m], c));
+      const uint32_t zk = bits_key16(penalise_member(mraw[q], cnt[m], c));
       mkey[m] = bits_key16(mraw[q]) | (zk << 16);
       zmax = max(zmax, zk);
       *bad |= is_nan_key16(zk) ? 1u : 0u;
@@ -428,80 +470,8 @@ __device__ __forceinline__ uint32_t member_keys(FastShared &sh, const uint32_t (
   return zmax;
 }
 
-// Rebuilds the member list and bitmap (after the full path reused their
-// space), with the raw logits fetched again.  Ends with a barrier.
-__device__ __forceinline__ void rebuild_members(FastShared &sh, const lmrs_sample_args &a, const RowCfg &c,
-                                                int64_t V, const uint16_t *rowp) {
-  uint32_t hid[kHistPer];
-  load_history_ids(hid, a, c);
-  clear_history(sh);
-  insert_history(sh, hid, c.h_len, V);
-  const uint32_t nmem = compact_members(sh);
-  uint32_t mraw[kMemPer], bad = 0u;
-  load_member_raw(mraw, sh, nmem, rowp);
-  member_keys(sh, mraw, nmem, c, &bad);
-  __syncthreads();
-}
-
 // ---- selection over LDS data ------------------------------------------------------
 
-// Chunk maxima of this thread's NCH chunk slots, two 16-bit keys per word
-// (slot s in the low half of cm[s / 2] when s is even).  They stay in
-// registers: every pass that filters on them reads them without latency.
-template <int NCH>
-struct ChunkMax {
-  uint32_t w[(NCH + 1) / 2];
-  __device__ __forceinline__ uint32_t get(int s) const { return (w[s >> 1] >> ((s & 1) * 16)) & 0xFFFFu; }
-};
-
-// The K-th largest value among the chunk maxima of the chunks without
-// history tokens (bit s of `mixed` set: slot s holds one) and the member z
-// keys -- each value stands for a distinct element whose z is at least the
-// value -- by a cascade of windows below `hi`, each twice as wide as the
-// last.  Returns false (uniformly) when fewer than K values exist.
-template <int NCH>
-__device__ __forceinline__ bool kth_value(FastShared &sh, const ChunkMax<NCH> &cm, bool roww, uint64_t mixed,
-                                          uint32_t nmem, uint32_t K, uint32_t hi, uint32_t *out) {
-  const int tid = threadIdx.x;
-  const uint32_t *mkey = sh.m_key();
-  uint32_t *wh = sh.whist();
-  uint32_t above = 0u, w = 64u;
-  for (;;) {
-    const uint32_t lo = hi >= w - 1u ? hi - (w - 1u) : 0u;
-    const uint32_t nbins = hi - lo + 1u;
-    for (uint32_t i = tid; i < nbins; i += kFT) wh[i] = 0u;
-    __syncthreads();
-    if (roww) {
-#pragma unroll
-      for (int s = 0; s < NCH; ++s) {
-        const uint32_t v = cm.get(s);
-        if (!((mixed >> s) & 1u) && v >= lo && v <= hi) atomicAdd(&wh[v - lo], 1u);
-      }
-    }
-    for (uint32_t m = tid; m < nmem; m += kFT) {
-      const uint32_t z = mkey[m] >> 16;
-      if (z >= lo && z <= hi) atomicAdd(&wh[z - lo], 1u);
-    }
-    __syncthreads();
-    const uint32_t mine = (uint32_t)tid < nbins ? wh[nbins - 1u - (uint32_t)tid] : 0u;  // bin hi - tid
-    uint32_t wtot;
-    const uint32_t ex = block_exclusive_scan<kFW>(mine, sh.uscr, &wtot);
-    if (above + wtot >= K) {
-      if (mine > 0u && above + ex < K && K <= above + ex + mine) sh.bsel[0] = hi - (uint32_t)tid;
-      __syncthreads();
-      *out = uniform(sh.bsel[0]);
-      return true;
-    }
-    if (lo == 0u) return false;
-    above += wtot;
-    hi = lo - 1u;
-    w = min(w * 2u, (uint32_t)kMaxWindow);
-  }
-}
-
-// Exact finish over the sorted candidates held one per lane of a wave (lane
-// i holds the i-th entry (~ykey << 32 | index), k <= 64 entries):
-// f64 weights exp(f64(l - max)), DPP prefix sums, the nucleus cut
 // (top_p.rs:45-58) and softmax_choice (strategies/mod.rs:27-55).
 template <class TR>
 __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const lmrs_sample_args &a, int r,
@@ -548,6 +518,108 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
   }
 }
 
+// Chunk maxima and member bits of every thread's slots, kept in LDS after the
+// load pass (slot-major words: word w of thread t at w * kFT + t).
+//   chunk maxima: two 16-bit keys per word (slot 2w low, 2w + 1 high)
+//   member bits:  four 8-bit masks per word (slot 4w + j in byte j)
+__device__ __forceinline__ uint32_t cm_word(const FastShared &sh, int w) {
+  return ((const uint32_t *)(sh.arena + kOffCm))[w * kFT + threadIdx.x];
+}
+__device__ __forceinline__ uint32_t hb_word(const FastShared &sh, int w) {
+  return ((const uint32_t *)(sh.arena + kOffHb))[w * kFT + threadIdx.x];
+}
+__device__ __forceinline__ uint32_t slot_m8(const FastShared &sh, int s) {
+  return (hb_word(sh, s >> 2) >> ((s & 3) * 8)) & 0xFFu;
+}
+// The member bits of chunk ch (any thread's).
+__device__ __forceinline__ uint32_t chunk_m8(const FastShared &sh, uint32_t ch) {
+  const uint32_t s = ch / kFT, t = ch % kFT;
+  return (((const uint32_t *)(sh.arena + kOffHb))[(s >> 2) * kFT + t] >> ((s & 3) * 8)) & 0xFFu;
+}
+
+// The K-th largest value among the chunk maxima of the chunks without
+// history tokens and the member z keys -- each value stands for a distinct
+// element whose z is at least the value -- by a cascade of windows below
+// `hi`, each twice as wide as the last.  Returns false (uniformly) when
+// fewer than K values exist.
+template <int NCH>
+__device__ __forceinline__ bool kth_value(FastShared &sh, uint32_t nmem, uint32_t K, uint32_t hi, uint32_t *out) {
+  const int tid = threadIdx.x;
+  const uint32_t *mkey = sh.m_key();
+  uint32_t *wh = sh.whist();
+  uint32_t above = 0u, w = 64u;
+  for (;;) {
+    const uint32_t lo = hi >= w - 1u ? hi - (w - 1u) : 0u;
+    const uint32_t nbins = hi - lo + 1u;
+    for (uint32_t i = tid; i < nbins; i += kFT) wh[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < NCH; ++s) {
+      const uint32_t v = (cm_word(sh, s >> 1) >> ((s & 1) * 16)) & 0xFFFFu;
+      if (slot_m8(sh, s) == 0u && v >= lo && v <= hi) atomicAdd(&wh[v - lo], 1u);
+    }
+    for (uint32_t m = tid; m < nmem; m += kFT) {
+      const uint32_t z = mkey[m] >> 16;
+      if (z >= lo && z <= hi) atomicAdd(&wh[z - lo], 1u);
+    }
+    __syncthreads();
+    const uint32_t mine = (uint32_t)tid < nbins ? wh[nbins - 1u - (uint32_t)tid] : 0u;  // bin hi - tid
+    uint32_t wtot;
+    const uint32_t ex = block_exclusive_scan<kFW>(mine, sh.uscr, &wtot);
+    if (above + wtot >= K) {
+      if (mine > 0u && above + ex < K && K <= above + ex + mine) sh.bsel[0] = hi - (uint32_t)tid;
+      __syncthreads();
+      *out = uniform(sh.bsel[0]);
+      return true;
+    }
+    if (lo == 0u) return false;
+    above += wtot;
+    hi = lo - 1u;
+    w = min(w * 2u, (uint32_t)kMaxWindow);
+  }
+}
+
+// The K-th largest of the block's thread values (0 = no value; hi and lo are
+// the largest and the smallest nonzero one), rounded down to the lower edge
+// of its bin when the values span more than kTvBins keys (bins of 2^s keys
+// counted down from hi).  The bins start at zero; every wave scans them
+// itself.  Returns false (uniformly) when fewer than K values exist.
+__device__ __forceinline__ bool kth_thread(FastShared &sh, uint32_t v, uint32_t hi, uint32_t lo, uint32_t K,
+                                           uint32_t *out) {
+  uint32_t *wh = sh.whist();
+  const uint32_t span = hi - lo;
+  const uint32_t s = span < (uint32_t)kTvBins ? 0u : 24u - (uint32_t)__builtin_clz(span);
+  if (v) atomicAdd(&wh[(hi - v) >> s], 1u);
+  __syncthreads();
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint4 b = ((const uint4 *)wh)[lane];  // bins 4 lane .. 4 lane + 3
+  const uint32_t own = b.x + b.y + b.z + b.w;
+  const uint32_t incl = wave_inclusive<OpSum>(own, 0u);
+  if (lane63(incl) < K) return false;
+  const uint32_t l = (uint32_t)__builtin_ctzll(__ballot(incl >= K));
+  const uint32_t acc = incl - own;
+  uint32_t bin = 4u * lane + 3u;
+  if (acc + b.x >= K)
+    bin = 4u * lane;
+  else if (acc + b.x + b.y >= K)
+    bin = 4u * lane + 1u;
+  else if (acc + b.x + b.y + b.z >= K)
+    bin = 4u * lane + 2u;
+  const uint32_t bstar = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)l);
+  const uint32_t drop = ((bstar + 1u) << s) - 1u;  // largest hi - v inside the bin
+  *out = uniform(span > drop ? hi - drop : lo);
+  return true;
+}
+
+// Bit e set: key e of the chunk (four packed words) is at least za.
+__device__ __forceinline__ uint32_t chunk_ge(const uint4 &w, uint32_t za) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+  uint32_t m = 0u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m |= (((x[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) >= za ? 1u : 0u) << e;
+  return m;
+}
+
 // ---- the ordered search of the full path ------------------------------------------
 
 // Net count change of a member for the range [lo, hi]: it leaves its raw key
@@ -579,30 +651,28 @@ template <int NCH>
 __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 *src, int nchunks, uint32_t nmem,
                                                     uint32_t lo, uint32_t hi, uint32_t j) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool roww = wave >= kHW;
-  const int rt = tid - 64 * kHW, rw = wave - kHW;  // row thread and row wave
   uint32_t *slot_cnt = sh.u32(kOffSlotCnt), *tcnt = sh.u32(kOffTcnt);
   const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
-  for (int i = tid; i < NCH * kRW; i += kFT) slot_cnt[i] = 0u;
+  for (int i = tid; i < NCH * kFW; i += kFT) slot_cnt[i] = 0u;
   __syncthreads();
-  if (roww) {
+  {
     constexpr int G = 8;  // slots in flight at a time
-    const int ft = fresh_tid() - 64 * kHW;
+    const int ft = fresh_tid();
 #pragma unroll
     for (int s0 = 0; s0 < NCH; s0 += G) {
       uint4 d[G];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const int ch = (s0 + g) * kRT + ft;
+        const int ch = (s0 + g) * kFT + ft;
         if (s0 + g < NCH) d[g] = *(ch < nchunks ? src + ch : &kNegInfChunk);
       }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int s = s0 + g;
         if (s < NCH) {
-          const uint32_t n = (s * kRT + ft < nchunks) ? chunk_matches(d[g], lo, hi) : 0u;
+          const uint32_t n = (s * kFT + ft < nchunks) ? chunk_matches(d[g], lo, hi) : 0u;
           const uint32_t t = wave_sum(n);
-          if (lane == 0 && t) atomicAdd(&slot_cnt[s * kRW + rw], t);
+          if (lane == 0 && t) atomicAdd(&slot_cnt[s * kFW + wave], t);
         }
       }
     }
@@ -610,12 +680,12 @@ __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 
   for (uint32_t m = tid; m < nmem; m += kFT) {
     const int dl = member_delta(mkey[m], lo, hi);
     const uint32_t ch = midx[m] >> 3;
-    if (dl) atomicAdd(&slot_cnt[(ch / kRT) * kRW + ((ch % kRT) >> 6)], (uint32_t)dl);
+    if (dl) atomicAdd(&slot_cnt[(ch / kFT) * kFW + ((ch % kFT) >> 6)], (uint32_t)dl);
   }
   __syncthreads();
   if (tid < NCH) {  // per-slot totals
     uint32_t tot = 0;
-    for (int w = 0; w < kRW; ++w) tot += slot_cnt[tid * kRW + w];
+    for (int w = 0; w < kFW; ++w) tot += slot_cnt[tid * kFW + w];
     tcnt[tid] = tot;
   }
   __syncthreads();
@@ -636,24 +706,21 @@ __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 
   __syncthreads();
   const int sstar = (int)uniform(sh.bsel[0]);
   const uint32_t jr = j - uniform(sh.bsel[1]);
-  if (roww) tcnt[rt] = 0u;
+  tcnt[tid] = 0u;
   if (tid < 8) sh.chunk_z[tid] = 0xFFFFFFFFu;
   __syncthreads();
   for (uint32_t m = tid; m < nmem; m += kFT) {  // members of slot sstar, per owner row thread
     const int dl = member_delta(mkey[m], lo, hi);
     const uint32_t ch = midx[m] >> 3;
-    if (dl && (int)(ch / kRT) == sstar) atomicAdd(&tcnt[ch % kRT], (uint32_t)dl);
+    if (dl && (int)(ch / kFT) == sstar) atomicAdd(&tcnt[ch % kFT], (uint32_t)dl);
   }
   __syncthreads();
-  const int chs = sstar * kRT + rt;
-  uint32_t mine = 0u;
-  if (roww) {
-    mine = tcnt[rt];
-    if (chs < nchunks) mine += chunk_matches(src[chs], lo, hi);
-  }
+  const int chs = sstar * kFT + tid;
+  uint32_t mine = tcnt[tid];
+  if (chs < nchunks) mine += chunk_matches(src[chs], lo, hi);
   uint32_t tot;
-  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);  // wave 0 adds zeros first
-  if (roww && excl < jr && jr <= excl + mine) {
+  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);
+  if (excl < jr && jr <= excl + mine) {
     sh.bsel[2] = (uint32_t)chs;  // the chunk
     sh.bsel[3] = jr - excl;      // rank inside it
   }
@@ -692,12 +759,11 @@ __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 
 template <int NCH>
 __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args &a, int r) {
   using TR = DTypeTraits<LMRS_DTYPE_BF16>;
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const bool roww = wave >= kHW;  // row thread
-  const int rt = tid - 64 * kHW;  // row thread index
+  const int tid = threadIdx.x;
   const int64_t V = a.vocab;
   const int nchunks = (int)(V >> 3);
-  const uint32_t npad = (uint32_t)(NCH * kRT - nchunks) * 8u;
+  const int nwords = (int)((V + 31) >> 5);
+  const uint32_t npad = (uint32_t)(NCH * kFT - nchunks) * 8u;
   const uint16_t *rowp = (const uint16_t *)((const char *)a.logits + (size_t)r * (size_t)a.row_stride * 2);
   const uint4 *src = (const uint4 *)rowp;
   u32x4 kv[NCH];
@@ -705,111 +771,186 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
 
   // Parameters through scalar loads (no store precedes them).  Then, in this
   // order: the history ids (requests queue in issue order across the whole
-  // chip: ids requested after 64 MB of logits would arrive after them), the
-  // first quarter of the row, the member build (hash, bitmap, member list)
-  // while that quarter streams in, the members' raw logits, the rest of the
-  // row.  A wave issuing loads faster than memory drains them stalls at the
-  // issue, so work placed after the last load would wait for most of the row.
-  // No path leaves before the load pass consumes the row.
+  // chip: ids requested after the logits would arrive after them), the first
+  // part of the row, the member tables (bitmap, rank map, multiplicities)
+  // while that part streams in, the members' raw logits, the rest of the
+  // row.  A wave issuing loads
+  // faster than memory drains them stalls at the issue, so work placed after
+  // the last load would wait for most of the row.  No path leaves before the
+  // load pass consumes the row.
   const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
   const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
   constexpr int kEarly = NCH / 4;
   uint32_t hid[kHistPer];
   if (hist) issue_history_ids(hid, a, c);
-  if (roww) {
 #pragma unroll
-    for (int s = 0; s < kEarly; ++s) {
-      const int ch = s * kRT + rt;
-      kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
-    }
+  for (int s = 0; s < kEarly; ++s) {
+    const int ch = s * kFT + tid;
+    kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
   }
+  clear_tables(sh, hist, nwords);
+  __syncthreads();
   uint32_t nmem = 0u;
   uint32_t mraw[kMemPer];
   if (hist) {
-    clear_history(sh);
 #pragma unroll
-    for (int q = 0; q < kHistPer; ++q) wait_loads<kEarly>(hid[q]);  // the first quarter stays in flight
-    insert_history(sh, hid, c.h_len, V);
-    nmem = compact_members(sh);
-    issue_member_raw(mraw, sh, nmem <= (uint32_t)kFastMembers ? nmem : 0u, rowp);
-  }
-  if (roww) {
-#pragma unroll
-    for (int s = kEarly; s < NCH; ++s) {
-      const int ch = s * kRT + rt;
-      kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);
+    for (int q = 0; q < kHistPer; ++q) wait_loads<kEarly>(hid[q]);  // the row's first part stays in flight
+    mark_history(sh, hid, c.h_len, V);
+    nmem = rank_members(sh, nwords);
+    if (nmem <= (uint32_t)kFastMembers) {
+      count_members(sh, hid, c.h_len, V);
+      issue_member_raw(mraw, sh, nmem, rowp);
     }
   }
+  const bool mem_ok = hist && nmem <= (uint32_t)kFastMembers;
+#pragma unroll
+  for (int s = kEarly; s < NCH; ++s) {
+    const int ch = s * kFT + tid;
+    kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);
+  }
+  uint32_t tv = 0u, mn = 0xFFFFFFFFu, bad = 0u;
 
-  // The load pass: raw keys, chunk maxima (all elements), the NaN check, and
-  // which elements are history tokens (8 bits per chunk, four chunks a word).
+  // The load pass: keys, chunk maxima, the NaN check, which elements are
+  // members (8 bits per chunk) and the thread value: the largest key of the
+  // chunks without members (raised to the members' z keys).  Chunk maxima
+  // and member bits go to LDS as their words fill.  The bitmap word of the
+  // next slot is read before waiting for this slot's data.
   const uint32_t *bitmap = sh.bitmap();
-  ChunkMax<NCH> cm;
-  uint32_t hbits[(NCH + 3) / 4];
-  uint64_t mixed = 0u;
-  uint32_t mx = 0u, mn = 0xFFFFFFFFu, bad = 0u;
-  if (roww) {
-    static_for<0, NCH>([&](auto S) {
-      constexpr int s = decltype(S)::value;
-      const int ch = s * kRT + rt;
-      wait_loads<NCH - 1 - s>(kv[s]);  // exact for the later loads, conservative for the first quarter
+  auto bitmap_word = [&](int s) {
+    const int ch = s * kFT + tid;
+    return bitmap[(ch < nchunks ? ch : nchunks - 1) >> 2];
+  };
+  uint32_t *cml = (uint32_t *)(sh.arena + kOffCm) + tid, *hbl = (uint32_t *)(sh.arena + kOffHb) + tid;
+  uint32_t cmw = 0u, hbw = 0u;
+  uint32_t bw = mem_ok ? bitmap_word(0) : 0u;
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    const int ch = s * kFT + tid;
+    const uint32_t bw_s = bw;
+    if constexpr (s + 1 < NCH) bw = mem_ok ? bitmap_word(s + 1) : 0u;
+    wait_loads<NCH - 1 - s>(kv[s]);  // exact for the later loads, conservative for the first part
+    if constexpr (s == kEarly) {
+      // The members' loads are older than this slot's: their keys are
+      // computed here, while the rest of the row streams in.
+      if (mem_ok) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t kp = key_pair(kv[s][q]);
-        k[s][q] = kp;
-        mn = pk_min_u16(mn, kp);
+        for (int q = 0; q < kMemPer; ++q) wait_loads<NCH - kEarly>(mraw[q]);
+        tv = max(tv, member_keys(sh, mraw, nmem, c, &bad));
       }
-      uint32_t cmx = chunk_max(k[s]);
-      bad |= cmx >= 0xFF81u ? 1u : 0u;
-      const bool valid = (s + 1) * kRT <= nchunks || ch < nchunks;
-      if (!valid) cmx = 0u;  // padding: no candidates
-      cm.w[s >> 1] = (s & 1) ? (cm.w[s >> 1] | (cmx << 16)) : cmx;
-      mx = max(mx, cmx);
-      uint32_t m8 = 0u;
-      if (hist && valid) m8 = (bitmap[ch >> 2] >> ((ch & 3) * 8)) & 0xFFu;
-      hbits[s >> 2] = (s & 3) ? (hbits[s >> 2] | (m8 << ((s & 3) * 8))) : m8;
-      mixed |= (uint64_t)(m8 != 0u) << s;
-    });
-    bad |= min(mn & 0xFFFFu, mn >> 16) <= 0x007Eu ? 1u : 0u;
-  }
-  if (hist && nmem <= (uint32_t)kFastMembers) {
+    }
 #pragma unroll
-    for (int q = 0; q < kMemPer; ++q) wait_loads<0>(mraw[q]);
-    mx = max(mx, member_keys(sh, mraw, nmem, c, &bad));
-  }
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t kp = key_pair(kv[s][q]);
+      k[s][q] = kp;
+      mn = pk_min_u16(mn, kp);
+    }
+    uint32_t cmx = chunk_max(k[s]);
+    bad |= cmx >= 0xFF81u ? 1u : 0u;
+    const bool valid = (s + 1) * kFT <= nchunks || ch < nchunks;
+    if (!valid) cmx = 0u;  // padding: no candidates
+    const uint32_t m8 = valid ? (bw_s >> ((ch & 3) * 8)) & 0xFFu : 0u;
+    tv = max(tv, m8 ? 0u : cmx);
+    cmw = (s & 1) ? (cmw | (cmx << 16)) : cmx;
+    if constexpr ((s & 1) == 1 || s == NCH - 1) cml[(s >> 1) * kFT] = cmw;
+    hbw = (s & 3) ? (hbw | (m8 << ((s & 3) * 8))) : m8;
+    if constexpr ((s & 3) == 3 || s == NCH - 1) hbl[(s >> 2) * kFT] = hbw;
+  });
+  bad |= min(mn & 0xFFFFu, mn >> 16) <= 0x007Eu ? 1u : 0u;
+
   if (c.status != LMRS_ROW_OK) {
     if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, c.status);
     return true;
   }
-  if (nmem > (uint32_t)kFastMembers) return false;
-  block_max2(mx, bad, sh);
+  if (hist && !mem_ok) return false;
+  uint32_t tvhi = tv, tvlo = tv ? ~tv : 0u;
+  block_max3(tvhi, tvlo, bad, sh);
   // Rows with a NaN go to the generic engine: the processors canonicalise
   // NaNs, which the key map does not model.
-  if (bad) return false;
-  const uint32_t ztop = mx;  // no z key of the row is larger
+  if (bad || tvhi == 0u) return false;
+  tvlo = ~tvlo;  // the smallest nonzero thread value
   const bool k_on = c.top_k > 0 && c.top_k < V;
   const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
   const uint4 *src2 = fresh(src);  // the re-reads of the full path
+  SelState &ss = sh.ss();
 
-  if (k_on && c.top_k <= kGatherCap) {  // ---- greedy and small k ----------------------
+  if (k_on && c.top_k <= kSmallK) {  // ---- greedy and small k ----------------------
     // Greedy (greedy.rs:22-29) is the case k = 1: the first of the sorted candidates.
     const uint32_t K = (uint32_t)c.top_k;
+    uint32_t L = tvhi;
+    if (K > 1u && !kth_thread(sh, tv, tvhi, tvlo, K, &L)) return false;
+    const uint32_t za = group_low(L, c);
+    // The chunks whose maximum reaches za are read again (each lane loops
+    // over its own few), and their elements at or above za (members
+    // excluded: they enter by their z key) become candidates, as do the
+    // members at or above za.  Entry: (~(y key << 16) << 32 | index), whose
+    // ascending order is the reference's sorted order.
+    uint64_t sm = 0u;
+    static_for<0, (NCH + 1) / 2>([&](auto W) {
+      constexpr int w = decltype(W)::value;
+      const uint32_t cw = cm_word(sh, w);
+      sm |= (uint64_t)((cw & 0xFFFFu) >= za ? 1u : 0u) << (2 * w);
+      if constexpr (2 * w + 1 < NCH) sm |= (uint64_t)((cw >> 16) >= za ? 1u : 0u) << (2 * w + 1);
+    });
+    uint32_t *ctr = sh.counters();
+    auto put = [&](uint32_t zk, uint32_t idx) {
+      const uint32_t p = atomicAdd(&ctr[1], 1u);
+      if (p < (uint32_t)kGatherCap) ss.gather[p] = ((uint64_t)(~(temp_key16(zk, c) << 16)) << 32) | idx;
+    };
+    const int ft = fresh_tid();
+    for (uint64_t m = sm; m; m &= m - 1ull) {
+      const uint32_t ch = (uint32_t)__builtin_ctzll(m) * kFT + (uint32_t)ft;
+      const uint4 d = src2[ch];
+      const uint4 w = make_uint4(key_pair(d.x), key_pair(d.y), key_pair(d.z), key_pair(d.w));
+      for (uint32_t e = chunk_ge(w, za) & ~chunk_m8(sh, ch); e; e &= e - 1u) {
+        const uint32_t el = (uint32_t)__builtin_ctz(e);
+        put(chunk_key(w, el), ch * 8u + el);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kMemPer; ++q) {
+      const uint32_t m = (uint32_t)tid + (uint32_t)q * kFT;
+      if (m < nmem && (mkey[m] >> 16) >= za) put(mkey[m] >> 16, midx[m]);
+    }
+    __syncthreads();
+    const uint32_t ncand = uniform(ctr[1]);
+    if (ncand > (uint32_t)kGatherCap) return false;
+    if (ncand <= (uint32_t)kFT) {
+      // Rank sort: candidate i moves to position (number of smaller
+      // candidates) when that is below 64; wave 0 finishes the first K.
+      uint64_t *sorted = (uint64_t *)sh.dump_keys();
+      if ((uint32_t)tid < ncand) {
+        const uint64_t g = ss.gather[tid];
+        uint32_t rank = 0u;
+#pragma unroll 8
+        for (uint32_t j = 0; j < ncand; ++j) rank += ss.gather[j] < g ? 1u : 0u;
+        if (rank < 64u) sorted[rank] = g;
+      }
+      __syncthreads();
+      if (tid < 64) finish_wave<TR>((uint32_t)tid < ncand ? sorted[tid] : ~0ull, c, a, r, K, K == 1u);
+      return true;
+    }
+    sort_gather<kFT>(ss, ncand);
+    finish_sorted<TR, kFT>(ss, c, a, r, K);
+    return true;
+  }
+
+  if (k_on && c.top_k <= kGatherCap) {  // ---- mid k -------------------------------
+    const uint32_t K = (uint32_t)c.top_k;
     uint32_t L;
-    if (!kth_value(sh, cm, roww, mixed, nmem, K, ztop, &L)) return false;
+    if (!kth_value<NCH>(sh, nmem, K, tvhi, &L)) return false;
     const uint32_t za = group_low(L, c);
     // gather every element with z >= za: (~(y key << 16) << 32 | index).
     // Count first (8-bit masks per candidate chunk, packed four to a word),
     // then one scan gives every thread its write offset: no atomics.
-    SelState &ss = sh.ss();
     uint32_t masks[(NCH + 3) / 4];
     uint32_t nmine = 0u;
     static_for<0, NCH>([&](auto S) {
       constexpr int s = decltype(S)::value;
       uint32_t m8 = 0u;
-      if (roww && cm.get(s) >= za) {
+      if (((cm_word(sh, s >> 1) >> ((s & 1) * 16)) & 0xFFFFu) >= za) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) m8 |= (((k[s][e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) >= za ? 1u : 0u) << e;
-        m8 &= ~(hbits[s >> 2] >> ((s & 3) * 8)) & 0xFFu;  // members enter by their z key
+        m8 &= ~slot_m8(sh, s);  // members enter by their z key
       }
       masks[s >> 2] = (s & 3) ? (masks[s >> 2] | (m8 << ((s & 3) * 8))) : m8;
       nmine += (uint32_t)__builtin_popcount(m8);
@@ -822,7 +963,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
         constexpr int s = decltype(S)::value;
         uint32_t m8 = (masks[s >> 2] >> ((s & 3) * 8)) & 0xFFu;
         if (m8) {
-          const uint32_t ch = (uint32_t)(s * kRT + rt);
+          const uint32_t ch = (uint32_t)(s * kFT + tid);
           const uint4 w = make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]);
           do {
             const uint32_t e = (uint32_t)__builtin_ctz(m8);
@@ -838,27 +979,13 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     }
     __syncthreads();
     if (ncand > (uint32_t)kGatherCap) return false;
-    if (ncand <= 64u) {
-      // rank sort inside wave 0: entry i moves to lane (number of smaller entries)
-      if (tid < 64) {
-        const uint64_t g = (uint32_t)tid < ncand ? ss.gather[tid] : ~0ull;
-        uint32_t rank = 0u;
-#pragma unroll 8
-        for (uint32_t j = 0; j < ncand; ++j) rank += ss.gather[j] < g ? 1u : 0u;
-        if ((uint32_t)tid >= ncand) rank = (uint32_t)tid;
-        const uint32_t lo32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)g);
-        const uint32_t hi32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)(g >> 32));
-        finish_wave<TR>(((uint64_t)hi32 << 32) | lo32, c, a, r, K, K == 1u);
-      }
-      return true;
-    }
     sort_gather<kFT>(ss, ncand);
     finish_sorted<TR, kFT>(ss, c, a, r, K);
     return true;
   }
 
   // ---- full: 65536-bin count histogram ------------------------------------------
-  __syncthreads();  // the hash, bitmap and window views are dead
+  __syncthreads();  // the bitmap, rank map, copy and window views are dead
   uint32_t *h64 = sh.u32(0);
   {
     uint4 *p = (uint4 *)h64;
@@ -870,12 +997,10 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     atomicAdd(&h64[ka & 0x7FFFu], (ka & 0x8000u) ? 0x10000u : 1u);
     atomicAdd(&h64[kb & 0x7FFFu], (kb & 0x8000u) ? 0x10000u : 1u);
   };
-  if (roww) {
 #pragma unroll
-    for (int s = 0; s < NCH; ++s) {
+  for (int s = 0; s < NCH; ++s) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) count_word(k[s][q]);
-    }
+    for (int q = 0; q < 4; ++q) count_word(k[s][q]);
   }
   __syncthreads();
   // members move from their raw key to their z key; padding leaves -inf
@@ -889,6 +1014,14 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     atomicSub(&h64[rk & 0x7FFFu], (rk & 0x8000u) ? 0x10000u : 1u);
   }
   if (tid == 0) atomicSub(&h64[kNegInfKey16], npad);
+  // The entries below overwrite the member list: it waits in registers.
+  uint32_t sv_idx[kMemPer], sv_key[kMemPer];
+#pragma unroll
+  for (int q = 0; q < kMemPer; ++q) {
+    const uint32_t m = (uint32_t)tid + (uint32_t)q * kFT;
+    sv_idx[q] = m < nmem ? midx[m] : 0u;
+    sv_key[q] = m < nmem ? mkey[m] : 0u;
+  }
   __syncthreads();
   // Compaction.  Thread t owns the KPT keys 65535-KPT*t .. 65536-KPT*(t+1)
   // (descending; position j holds key 65535-KPT*t-j): the high halves of
@@ -1054,7 +1187,18 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   const float yv = key16_value(ykey_of(h));
   const bool first_tok = (h == 0 && jt == 1u), last_tok = (h == last_h && jt == gmax);
   __syncthreads();  // entries and prefixes are dead
-  if (nmem) rebuild_members(sh, a, c, V, rowp);
+  if (nmem) {
+    uint32_t *wi = sh.m_idx(), *wk = sh.m_key();
+#pragma unroll
+    for (int q = 0; q < kMemPer; ++q) {
+      const uint32_t m = (uint32_t)tid + (uint32_t)q * kFT;
+      if (m < nmem) {
+        wi[m] = sv_idx[q];
+        wk[m] = sv_key[q];
+      }
+    }
+    __syncthreads();
+  }
   const uint32_t token = find_jth_stream<NCH>(sh, src2, nchunks, nmem, zlo, zhi, jt);
   if (tid == 0) {
     const double lo_c = (mx2 + (double)(jt - 1u) * wg) / kept_mass, hi_c = lo_c + wg / kept_mass;

@@ -39,12 +39,12 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
     // register-resident rows: NCH chunks of 8 logits per thread (rows the
     // fast path does not take finish in the generic engine, in the same launch)
     const dim3 grid(args->batch), block(lmrs::kFT);
-    constexpr int kRowsPerSlot = 8 * lmrs::kRT;  // logits per chunk slot of the row threads
-    if (V <= 8 * kRowsPerSlot)
+    constexpr int kSlot = 8 * lmrs::kFT;  // logits per chunk slot (one 16-byte chunk per thread)
+    if (V <= 8 * kSlot)
       lmrs::bf16_fast_kernel<8><<<grid, block, 0, s>>>(*args);
-    else if (V <= 16 * kRowsPerSlot)
+    else if (V <= 16 * kSlot)
       lmrs::bf16_fast_kernel<16><<<grid, block, 0, s>>>(*args);
-    else if (V <= 32 * kRowsPerSlot)
+    else if (V <= 32 * kSlot)
       lmrs::bf16_fast_kernel<32><<<grid, block, 0, s>>>(*args);
     else
       lmrs::bf16_fast_kernel<lmrs::kMaxSlots><<<grid, block, 0, s>>>(*args);
