@@ -66,6 +66,7 @@ constexpr int kDumpCap = 1024;      // chunks the thread-value path copies to LD
 
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Loads of the row and of the history ids are issued through inline assembly
@@ -155,8 +156,9 @@ __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
 // Order keys of two packed bf16 values: flip all bits of negatives, set the
 // sign bit of non-negatives (per 16-bit half).
 __device__ __forceinline__ uint32_t key_pair(uint32_t w) {
-  const uint32_t sgn = (w >> 15) & 0x00010001u;
-  return w ^ (sgn * 0x7FFFu + 0x80008000u);
+  const uint32_t neg = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, w) >> (short)15);  // 0xFFFF per negative half
+  // w ^ (neg | 0x80008000): truth table of a ^ (b | c) over a = 0xF0, b = 0xCC, c = 0xAA
+  return __builtin_amdgcn_bitop3_b32(w, neg, 0x80008000u, (uint8_t)(0xF0 ^ (0xCC | 0xAA)));
 }
 
 __device__ __forceinline__ uint32_t key16_bits(uint32_t k) {
@@ -225,42 +227,39 @@ __device__ __forceinline__ uint32_t penalise_member(uint32_t raw, uint32_t count
 //   the entries (key << 16 | count) and [0, 72K) their prefixes; for the
 //   final search the member list is rebuilt and [128K, 134K) holds the
 // LDS arena with phase-dependent views (byte offsets):
-//   [0, 40K)      chunk maxima of the load pass (then SelState)
-//   [0, 57K)      SelState: candidate list, sort and finish scratch
+//   [0, 10K)      per bitmap word, the number of members before it (history
+//                 build); then [0, 57K) SelState: candidate list, sort and
+//                 finish scratch
 //   [60K, 62K)    window histogram (thread values; count cascade)
 //   [62K, 62K+64) counters of the small-k path
-//   [64K, 84K)    membership bitmap over the vocab (history build); then the
-//                 chunks copied by the small-k path: keys [64K, 80K),
-//                 chunk index | member bits << 24 [80K, 84K)
-//   [84K, 124K)   rank map: per bitmap word, (members before it, the word)
-//                 (history build); then the member bits of the load pass
+//   [64K, 84K)    membership bitmap over the vocab; bits 8 (c & 3) .. 8 (c & 3)
+//                 + 7 of word c / 4 are chunk c's members; then the partial
+//                 ranks of the small-k finish
+//   [84K, 124K)   chunk maxima of the load pass (word w of thread t at
+//                 w * kFT + t: slots 2w, 2w + 1)
 //   [128K, 152K)  members: token ids, multiplicities, raw key | z key << 16
 //   full path: [0, 128K) 65536 16-bit counters; after compaction [128K, 152K)
 //   the entries (key << 16 | count) -- the member list waits in registers
 //   meanwhile -- and [0, 72K) their prefixes; the ordered search keeps its
 //   per-slot / per-thread counts at [0, 4K)
 constexpr int kArenaBytes = 152 * 1024;
+constexpr int kOffPrefix = 0;
 constexpr int kOffWhist = 60 * 1024;
 constexpr int kOffCounters = 62 * 1024;
 constexpr int kOffBitmap = 64 * 1024;
-constexpr int kOffDumpKeys = 64 * 1024;
-constexpr int kOffDumpMeta = 80 * 1024;
-constexpr int kOffRankMap = 84 * 1024;
+constexpr int kOffRankScratch = 64 * 1024;
+constexpr int kOffCm = 84 * 1024;
 constexpr int kOffMembers = 128 * 1024;
 constexpr int kOffEntries = 128 * 1024;
-constexpr int kOffCm = 0;
-constexpr int kOffHb = kOffRankMap;
 constexpr int kOffSlotCnt = 0;
 constexpr int kOffTcnt = kMaxSlots * kFW * 4;
+static_assert(kOffPrefix + kMaxWords * 2 <= kOffWhist, "prefix view");
 static_assert((int)sizeof(SelState) <= kOffWhist, "SelState view");
 static_assert(kOffWhist + kMaxWindow * 4 <= kOffCounters && kTvBins <= kMaxWindow, "window view");
 static_assert(kOffCounters + 64 <= kOffBitmap, "counter view");
-static_assert(kOffBitmap + kMaxWords * 4 <= kOffRankMap, "bitmap view");
-static_assert(kOffDumpKeys + kDumpCap * 16 <= kOffDumpMeta && kOffDumpMeta + kDumpCap * 4 <= kOffRankMap,
-              "chunk copy view");
-static_assert(kOffRankMap + kMaxWords * 8 <= kOffMembers, "rank map view");
-static_assert(kOffCm + kMaxSlots / 2 * kFT * 4 <= kOffWhist, "chunk maxima view");
-static_assert(kOffHb + kMaxSlots / 4 * kFT * 4 <= kOffMembers, "member bits view");
+static_assert(kOffBitmap + kMaxWords * 4 <= kOffCm, "bitmap view");
+static_assert(kOffRankScratch + kFT * 4 <= kOffCm, "rank view");
+static_assert(kOffCm + kMaxSlots / 2 * kFT * 4 <= kOffMembers, "chunk maxima view");
 static_assert(kOffMembers + kFastMembers * 12 <= kArenaBytes, "member view");
 static_assert(kOffEntries + kMaxEntries * 4 <= kArenaBytes, "entries view");
 static_assert(kMaxEntries * 12 <= kOffEntries, "prefix view");
@@ -282,11 +281,10 @@ struct FastShared {
   __device__ uint32_t *m_cnt() { return u32(kOffMembers + kFastMembers * 4); }
   __device__ uint32_t *m_key() { return u32(kOffMembers + kFastMembers * 8); }
   __device__ uint32_t *bitmap() { return u32(kOffBitmap); }
-  __device__ uint2 *rank_map() { return (uint2 *)(arena + kOffRankMap); }
+  __device__ uint16_t *prefix() { return (uint16_t *)(arena + kOffPrefix); }
   __device__ uint32_t *whist() { return u32(kOffWhist); }
   __device__ uint32_t *counters() { return u32(kOffCounters); }
-  __device__ uint4 *dump_keys() { return (uint4 *)(arena + kOffDumpKeys); }
-  __device__ uint32_t *dump_meta() { return u32(kOffDumpMeta); }
+  __device__ uint32_t *rank_scratch() { return u32(kOffRankScratch); }
   __device__ SelState &ss() { return *(SelState *)(arena); }
 };
 
@@ -375,10 +373,12 @@ __device__ __forceinline__ void clear_tables(FastShared &sh, bool hist, int nwor
   }
 }
 
-// Marks the history ids below V in the bitmap.  Ends with a barrier.
+// Marks the history ids below V in the bitmap.  Starts and ends with a
+// barrier (the bitmap was cleared without one).
 __device__ __forceinline__ void mark_history(FastShared &sh, const uint32_t (&hid)[kHistPer], int64_t h_len,
                                              int64_t V) {
   uint32_t *bm = sh.bitmap();
+  __syncthreads();
 #pragma unroll
   for (int q = 0; q < kHistPer; ++q) {
     const uint32_t t = hid[q];
@@ -387,50 +387,51 @@ __device__ __forceinline__ void mark_history(FastShared &sh, const uint32_t (&hi
   __syncthreads();
 }
 
-// The rank map: for bitmap word w, (the number of members with a token below
-// 32 w, the word).  Thread t owns words kWordsPer * t ... kWordsPer * t +
+// Member indices in token order: prefix[w] = the number of members with a
+// token below 32 w.  Thread t owns words kWordsPer * t ... kWordsPer * t +
 // kWordsPer - 1, so one block scan orders them.  Returns the member count
 // (uniform).  Ends with a barrier.
 __device__ __forceinline__ uint32_t rank_members(FastShared &sh, int nwords) {
   const int tid = threadIdx.x;
   const uint32_t *bm = sh.bitmap();
-  uint2 *rm = sh.rank_map();
-  uint32_t w[kWordsPer];
-  uint32_t n = 0u;
+  uint16_t *pre = sh.prefix();
+  uint32_t n[kWordsPer];
+  uint32_t tot = 0u;
 #pragma unroll
   for (int i = 0; i < kWordsPer; ++i) {
     const int j = tid * kWordsPer + i;
-    w[i] = j < nwords ? bm[j] : 0u;
-    n += (uint32_t)__builtin_popcount(w[i]);
+    n[i] = j < nwords ? (uint32_t)__builtin_popcount(bm[j]) : 0u;
+    tot += n[i];
   }
   uint32_t total;
-  uint32_t p = block_exclusive_scan<kFW>(n, sh.uscr, &total);
+  uint32_t p = block_exclusive_scan<kFW>(tot, sh.uscr, &total);
 #pragma unroll
   for (int i = 0; i < kWordsPer; ++i) {
     const int j = tid * kWordsPer + i;
-    if (j < nwords) rm[j] = make_uint2(p, w[i]);
-    p += (uint32_t)__builtin_popcount(w[i]);
+    if (j < nwords) pre[j] = (uint16_t)p;
+    p += n[i];
   }
   __syncthreads();
   return total;
 }
 
-// Index of member t (a marked token) in token order.
-__device__ __forceinline__ uint32_t member_rank(const uint2 &e, uint32_t bit) {
-  return e.x + (uint32_t)__builtin_popcount(e.y & ((1u << bit) - 1u));
+// Index of member t in token order.
+__device__ __forceinline__ uint32_t member_rank(const FastShared &sh, uint32_t t) {
+  const uint32_t w = ((const uint32_t *)(sh.arena + kOffBitmap))[t >> 5];
+  return (uint32_t)((const uint16_t *)(sh.arena + kOffPrefix))[t >> 5] +
+         (uint32_t)__builtin_popcount(w & ((1u << (t & 31u)) - 1u));
 }
 
 // Token ids and multiplicities of the members, at their indices.  Ends with
 // a barrier.
 __device__ __forceinline__ void count_members(FastShared &sh, const uint32_t (&hid)[kHistPer], int64_t h_len,
                                               int64_t V) {
-  const uint2 *rm = sh.rank_map();
   uint32_t *cnt = sh.m_cnt(), *midx = sh.m_idx();
 #pragma unroll
   for (int q = 0; q < kHistPer; ++q) {
     const uint32_t t = hid[q];
     if (history_live(q, t, h_len, V)) {
-      const uint32_t m = member_rank(rm[t >> 5], t & 31u);
+      const uint32_t m = member_rank(sh, t);
       atomicAdd(&cnt[m], 1u);
       midx[m] = t;  // every copy of a token writes the same id
     }
@@ -518,32 +519,24 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
   }
 }
 
-// Chunk maxima and member bits of every thread's slots, kept in LDS after the
-// load pass (slot-major words: word w of thread t at w * kFT + t).
-//   chunk maxima: two 16-bit keys per word (slot 2w low, 2w + 1 high)
-//   member bits:  four 8-bit masks per word (slot 4w + j in byte j)
+// Chunk maxima of every thread's slots, kept in LDS after the load pass:
+// word w of thread t at w * kFT + t holds slots 2w (low half) and 2w + 1.
 __device__ __forceinline__ uint32_t cm_word(const FastShared &sh, int w) {
   return ((const uint32_t *)(sh.arena + kOffCm))[w * kFT + threadIdx.x];
 }
-__device__ __forceinline__ uint32_t hb_word(const FastShared &sh, int w) {
-  return ((const uint32_t *)(sh.arena + kOffHb))[w * kFT + threadIdx.x];
-}
-__device__ __forceinline__ uint32_t slot_m8(const FastShared &sh, int s) {
-  return (hb_word(sh, s >> 2) >> ((s & 3) * 8)) & 0xFFu;
-}
-// The member bits of chunk ch (any thread's).
+// The member bits of chunk ch (eight logits: byte ch & 3 of bitmap word ch / 4).
 __device__ __forceinline__ uint32_t chunk_m8(const FastShared &sh, uint32_t ch) {
-  const uint32_t s = ch / kFT, t = ch % kFT;
-  return (((const uint32_t *)(sh.arena + kOffHb))[(s >> 2) * kFT + t] >> ((s & 3) * 8)) & 0xFFu;
+  return (((const uint32_t *)(sh.arena + kOffBitmap))[ch >> 2] >> ((ch & 3u) * 8u)) & 0xFFu;
 }
 
 // The K-th largest value among the chunk maxima of the chunks without
-// history tokens and the member z keys -- each value stands for a distinct
+// history tokens (hist: a bitmap exists) and the member z keys -- each value stands for a distinct
 // element whose z is at least the value -- by a cascade of windows below
 // `hi`, each twice as wide as the last.  Returns false (uniformly) when
 // fewer than K values exist.
 template <int NCH>
-__device__ __forceinline__ bool kth_value(FastShared &sh, uint32_t nmem, uint32_t K, uint32_t hi, uint32_t *out) {
+__device__ __forceinline__ bool kth_value(FastShared &sh, bool hist, uint32_t nmem, uint32_t K, uint32_t hi,
+                                          uint32_t *out) {
   const int tid = threadIdx.x;
   const uint32_t *mkey = sh.m_key();
   uint32_t *wh = sh.whist();
@@ -556,7 +549,8 @@ __device__ __forceinline__ bool kth_value(FastShared &sh, uint32_t nmem, uint32_
 #pragma unroll
     for (int s = 0; s < NCH; ++s) {
       const uint32_t v = (cm_word(sh, s >> 1) >> ((s & 1) * 16)) & 0xFFFFu;
-      if (slot_m8(sh, s) == 0u && v >= lo && v <= hi) atomicAdd(&wh[v - lo], 1u);
+      const bool mixed = hist && chunk_m8(sh, (uint32_t)(s * kFT + tid)) != 0u;
+      if (!mixed && v >= lo && v <= hi) atomicAdd(&wh[v - lo], 1u);
     }
     for (uint32_t m = tid; m < nmem; m += kFT) {
       const uint32_t z = mkey[m] >> 16;
@@ -580,35 +574,46 @@ __device__ __forceinline__ bool kth_value(FastShared &sh, uint32_t nmem, uint32_
 }
 
 // The K-th largest of the block's thread values (0 = no value; hi and lo are
-// the largest and the smallest nonzero one), rounded down to the lower edge
-// of its bin when the values span more than kTvBins keys (bins of 2^s keys
-// counted down from hi).  The bins start at zero; every wave scans them
-// itself.  Returns false (uniformly) when fewer than K values exist.
+// the largest and the smallest nonzero one).  First from one-key bins over
+// the kTvBins keys below hi; when fewer than K values lie there, from bins
+// of 2^s keys over [lo, hi], rounded down to the lower edge of its bin.
+// The bins start at zero; every wave scans them itself.  Returns false
+// (uniformly) when fewer than K values exist.
 __device__ __forceinline__ bool kth_thread(FastShared &sh, uint32_t v, uint32_t hi, uint32_t lo, uint32_t K,
                                            uint32_t *out) {
   uint32_t *wh = sh.whist();
+  const uint32_t lane = threadIdx.x & 63u;
+  // The bin holding the K-th count (counting from bin 0), its lower edge
+  // hi - (((bin + 1) << s) - 1); false when the bins hold fewer than K.
+  auto scan = [&](uint32_t s, uint32_t *edge) {
+    const uint4 b = ((const uint4 *)wh)[lane];  // bins 4 lane .. 4 lane + 3
+    const uint32_t own = b.x + b.y + b.z + b.w;
+    const uint32_t incl = wave_inclusive<OpSum>(own, 0u);
+    if (lane63(incl) < K) return false;
+    const uint32_t l = (uint32_t)__builtin_ctzll(__ballot(incl >= K));
+    const uint32_t acc = incl - own;
+    uint32_t bin = 4u * lane + 3u;
+    if (acc + b.x >= K)
+      bin = 4u * lane;
+    else if (acc + b.x + b.y >= K)
+      bin = 4u * lane + 1u;
+    else if (acc + b.x + b.y + b.z >= K)
+      bin = 4u * lane + 2u;
+    const uint32_t drop = (((uint32_t)__builtin_amdgcn_readlane((int)bin, (int)l) + 1u) << s) - 1u;
+    *edge = uniform(hi - lo > drop ? hi - drop : lo);
+    return true;
+  };
+  if (v && hi - v < (uint32_t)kTvBins) atomicAdd(&wh[hi - v], 1u);
+  __syncthreads();
+  if (scan(0u, out)) return true;
+  __syncthreads();  // every wave has read the bins
+  if (threadIdx.x < (unsigned)kTvBins) wh[threadIdx.x] = 0u;
+  __syncthreads();
   const uint32_t span = hi - lo;
   const uint32_t s = span < (uint32_t)kTvBins ? 0u : 24u - (uint32_t)__builtin_clz(span);
   if (v) atomicAdd(&wh[(hi - v) >> s], 1u);
   __syncthreads();
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint4 b = ((const uint4 *)wh)[lane];  // bins 4 lane .. 4 lane + 3
-  const uint32_t own = b.x + b.y + b.z + b.w;
-  const uint32_t incl = wave_inclusive<OpSum>(own, 0u);
-  if (lane63(incl) < K) return false;
-  const uint32_t l = (uint32_t)__builtin_ctzll(__ballot(incl >= K));
-  const uint32_t acc = incl - own;
-  uint32_t bin = 4u * lane + 3u;
-  if (acc + b.x >= K)
-    bin = 4u * lane;
-  else if (acc + b.x + b.y >= K)
-    bin = 4u * lane + 1u;
-  else if (acc + b.x + b.y + b.z >= K)
-    bin = 4u * lane + 2u;
-  const uint32_t bstar = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)l);
-  const uint32_t drop = ((bstar + 1u) << s) - 1u;  // largest hi - v inside the bin
-  *out = uniform(span > drop ? hi - drop : lo);
-  return true;
+  return scan(s, out);
 }
 
 // Bit e set: key e of the chunk (four packed words) is at least za.
@@ -769,75 +774,47 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   u32x4 kv[NCH];
   uint32_t k[NCH][4];
 
-  // Parameters through scalar loads (no store precedes them).  Then, in this
-  // order: the history ids (requests queue in issue order across the whole
-  // chip: ids requested after the logits would arrive after them), the first
-  // part of the row, the member tables (bitmap, rank map, multiplicities)
-  // while that part streams in, the members' raw logits, the rest of the
-  // row.  A wave issuing loads
-  // faster than memory drains them stalls at the issue, so work placed after
-  // the last load would wait for most of the row.  No path leaves before the
-  // load pass consumes the row.
+  // Parameters through scalar loads (no store precedes them), then the
+  // history ids (requests queue in issue order across the whole chip: ids
+  // requested after the logits would arrive after them) and the row's first
+  // kEarly slots.  The load pass requests slot s + kEarly when it processes
+  // slot s, so that a wave never waits long on a full memory queue with
+  // data at hand.  The member tables are built inside the load pass, after
+  // slot kHistAt, while the row streams in; the members' raw logits are
+  // requested right after them and their keys computed kEarly + 1 slots
+  // later.  No path leaves before the load pass consumes the row.
   const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
   const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
-  constexpr int kEarly = NCH / 4;
+  constexpr int kEarly = NCH / 4;     // slots in flight ahead of the one being processed
+  constexpr int kHistAt = 2;          // the slot after which the member tables are built
+  constexpr int kKeysAt = kHistAt + kEarly + 1;  // the slot whose wait covers the members' loads
+  static_assert(kKeysAt < NCH, "member keys inside the load pass");
+  auto issue_slot = [&](int s) {
+    const int ch = s * kFT + tid;
+    return issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
+  };
   uint32_t hid[kHistPer];
   if (hist) issue_history_ids(hid, a, c);
 #pragma unroll
-  for (int s = 0; s < kEarly; ++s) {
-    const int ch = s * kFT + tid;
-    kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
-  }
+  for (int s = 0; s < kEarly; ++s) kv[s] = issue_slot(s);
   clear_tables(sh, hist, nwords);
-  __syncthreads();
-  uint32_t nmem = 0u;
-  uint32_t mraw[kMemPer];
-  if (hist) {
-#pragma unroll
-    for (int q = 0; q < kHistPer; ++q) wait_loads<kEarly>(hid[q]);  // the row's first part stays in flight
-    mark_history(sh, hid, c.h_len, V);
-    nmem = rank_members(sh, nwords);
-    if (nmem <= (uint32_t)kFastMembers) {
-      count_members(sh, hid, c.h_len, V);
-      issue_member_raw(mraw, sh, nmem, rowp);
-    }
-  }
-  const bool mem_ok = hist && nmem <= (uint32_t)kFastMembers;
-#pragma unroll
-  for (int s = kEarly; s < NCH; ++s) {
-    const int ch = s * kFT + tid;
-    kv[s] = issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);
-  }
-  uint32_t tv = 0u, mn = 0xFFFFFFFFu, bad = 0u;
 
-  // The load pass: keys, chunk maxima, the NaN check, which elements are
-  // members (8 bits per chunk) and the thread value: the largest key of the
-  // chunks without members (raised to the members' z keys).  Chunk maxima
-  // and member bits go to LDS as their words fill.  The bitmap word of the
-  // next slot is read before waiting for this slot's data.
-  const uint32_t *bitmap = sh.bitmap();
-  auto bitmap_word = [&](int s) {
-    const int ch = s * kFT + tid;
-    return bitmap[(ch < nchunks ? ch : nchunks - 1) >> 2];
-  };
-  uint32_t *cml = (uint32_t *)(sh.arena + kOffCm) + tid, *hbl = (uint32_t *)(sh.arena + kOffHb) + tid;
-  uint32_t cmw = 0u, hbw = 0u;
-  uint32_t bw = mem_ok ? bitmap_word(0) : 0u;
+  // The load pass: keys, chunk maxima (to LDS as their words fill), the NaN
+  // check, and the largest chunk maximum with its slot and keys.
+  uint32_t *cml = (uint32_t *)(sh.arena + kOffCm) + tid;
+  uint32_t cmw = 0u, mn = 0xFFFFFFFFu, mx = 0u, s1 = 0u, bad = 0u, zmem = 0u, nmem = 0u;
+  uint32_t b0 = 0u, b1 = 0u, b2 = 0u, b3 = 0u;  // the keys of chunk s1
+  bool mem_ok = false;
+  uint32_t mraw[kMemPer];
   static_for<0, NCH>([&](auto S) {
     constexpr int s = decltype(S)::value;
     const int ch = s * kFT + tid;
-    const uint32_t bw_s = bw;
-    if constexpr (s + 1 < NCH) bw = mem_ok ? bitmap_word(s + 1) : 0u;
-    wait_loads<NCH - 1 - s>(kv[s]);  // exact for the later loads, conservative for the first part
-    if constexpr (s == kEarly) {
-      // The members' loads are older than this slot's: their keys are
-      // computed here, while the rest of the row streams in.
-      if (mem_ok) {
-#pragma unroll
-        for (int q = 0; q < kMemPer; ++q) wait_loads<NCH - kEarly>(mraw[q]);
-        tv = max(tv, member_keys(sh, mraw, nmem, c, &bad));
-      }
-    }
+    if constexpr (s + kEarly < NCH) kv[s + kEarly] = issue_slot(s + kEarly);
+    // loads issued after slot s's: later slots, and the members' for the
+    // slots issued before them and waited for after them
+    constexpr int younger =
+        (s + kEarly < NCH ? s + kEarly : NCH - 1) - s + (s > kHistAt && s <= kHistAt + kEarly ? kMemPer : 0);
+    wait_loads<younger>(kv[s]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t kp = key_pair(kv[s][q]);
@@ -845,16 +822,42 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
       mn = pk_min_u16(mn, kp);
     }
     uint32_t cmx = chunk_max(k[s]);
-    bad |= cmx >= 0xFF81u ? 1u : 0u;
     const bool valid = (s + 1) * kFT <= nchunks || ch < nchunks;
     if (!valid) cmx = 0u;  // padding: no candidates
-    const uint32_t m8 = valid ? (bw_s >> ((ch & 3) * 8)) & 0xFFu : 0u;
-    tv = max(tv, m8 ? 0u : cmx);
+    const bool top = cmx > mx;  // selects, not branches
+    s1 = top ? (uint32_t)s : s1;
+    b0 = top ? k[s][0] : b0;
+    b1 = top ? k[s][1] : b1;
+    b2 = top ? k[s][2] : b2;
+    b3 = top ? k[s][3] : b3;
+    // made here, while the wave waits for memory anyway (left to itself, the
+    // compiler keeps the 32 conditions and selects after the pass)
+    asm volatile("" : "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3), "+v"(s1));
+    mx = max(mx, cmx);
     cmw = (s & 1) ? (cmw | (cmx << 16)) : cmx;
     if constexpr ((s & 1) == 1 || s == NCH - 1) cml[(s >> 1) * kFT] = cmw;
-    hbw = (s & 3) ? (hbw | (m8 << ((s & 3) * 8))) : m8;
-    if constexpr ((s & 3) == 3 || s == NCH - 1) hbl[(s >> 2) * kFT] = hbw;
+    if constexpr (s == kHistAt) {
+      // the history ids are older than this slot's loads: complete
+      if (hist) {
+#pragma unroll
+        for (int q = 0; q < kHistPer; ++q) wait_loads<younger>(hid[q]);
+        mark_history(sh, hid, c.h_len, V);
+        nmem = rank_members(sh, nwords);
+        if (nmem <= (uint32_t)kFastMembers) count_members(sh, hid, c.h_len, V);
+      }
+      mem_ok = hist && nmem <= (uint32_t)kFastMembers;
+      issue_member_raw(mraw, sh, mem_ok ? nmem : 0u, rowp);  // always kMemPer loads: fixed wait counts
+    }
+    if constexpr (s == kKeysAt) {
+      // Every explicitly issued load is waited for on every path: until its
+      // wait, the compiler keeps the destination register for it (a load
+      // left unwaited could land in a register already reused).
+#pragma unroll
+      for (int q = 0; q < kMemPer; ++q) wait_loads<younger>(mraw[q]);
+      if (mem_ok) zmem = member_keys(sh, mraw, nmem, c, &bad);
+    }
   });
+  bad |= mx >= 0xFF81u ? 1u : 0u;
   bad |= min(mn & 0xFFFFu, mn >> 16) <= 0x007Eu ? 1u : 0u;
 
   if (c.status != LMRS_ROW_OK) {
@@ -862,6 +865,12 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     return true;
   }
   if (hist && !mem_ok) return false;
+  // The thread value: the largest chunk maximum when that chunk holds no
+  // member (else none), raised to the members' z keys -- each a distinct
+  // element's key.
+  const int ft = fresh_tid();
+  const uint32_t ch1 = s1 * kFT + (uint32_t)ft;
+  const uint32_t tv = max((hist && chunk_m8(sh, ch1) != 0u) ? 0u : mx, zmem);
   uint32_t tvhi = tv, tvlo = tv ? ~tv : 0u;
   block_max3(tvhi, tvlo, bad, sh);
   // Rows with a NaN go to the generic engine: the processors canonicalise
@@ -870,7 +879,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   tvlo = ~tvlo;  // the smallest nonzero thread value
   const bool k_on = c.top_k > 0 && c.top_k < V;
   const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
-  const uint4 *src2 = fresh(src);  // the re-reads of the full path
+  const uint4 *src2 = fresh(src);  // the re-reads
   SelState &ss = sh.ss();
 
   if (k_on && c.top_k <= kSmallK) {  // ---- greedy and small k ----------------------
@@ -879,32 +888,38 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     uint32_t L = tvhi;
     if (K > 1u && !kth_thread(sh, tv, tvhi, tvlo, K, &L)) return false;
     const uint32_t za = group_low(L, c);
-    // The chunks whose maximum reaches za are read again (each lane loops
-    // over its own few), and their elements at or above za (members
-    // excluded: they enter by their z key) become candidates, as do the
-    // members at or above za.  Entry: (~(y key << 16) << 32 | index), whose
-    // ascending order is the reference's sorted order.
+    // The chunks whose maximum reaches za give their elements at or above
+    // za (members excluded: they enter by their z key) as candidates, as do
+    // the members at or above za.  Entry: (~(y key << 16) << 32 | index),
+    // whose ascending order is the reference's sorted order.
+    uint32_t cw[(NCH + 1) / 2];
+#pragma unroll
+    for (int w = 0; w < (NCH + 1) / 2; ++w) cw[w] = cm_word(sh, w);  // all reads in flight together
     uint64_t sm = 0u;
-    static_for<0, (NCH + 1) / 2>([&](auto W) {
-      constexpr int w = decltype(W)::value;
-      const uint32_t cw = cm_word(sh, w);
-      sm |= (uint64_t)((cw & 0xFFFFu) >= za ? 1u : 0u) << (2 * w);
-      if constexpr (2 * w + 1 < NCH) sm |= (uint64_t)((cw >> 16) >= za ? 1u : 0u) << (2 * w + 1);
+    static_for<0, NCH>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      sm |= (uint64_t)(((cw[s >> 1] >> (16 * (s & 1))) & 0xFFFFu) >= za ? 1u : 0u) << s;
     });
     uint32_t *ctr = sh.counters();
     auto put = [&](uint32_t zk, uint32_t idx) {
       const uint32_t p = atomicAdd(&ctr[1], 1u);
       if (p < (uint32_t)kGatherCap) ss.gather[p] = ((uint64_t)(~(temp_key16(zk, c) << 16)) << 32) | idx;
     };
-    const int ft = fresh_tid();
-    for (uint64_t m = sm; m; m &= m - 1ull) {
-      const uint32_t ch = (uint32_t)__builtin_ctzll(m) * kFT + (uint32_t)ft;
-      const uint4 d = src2[ch];
-      const uint4 w = make_uint4(key_pair(d.x), key_pair(d.y), key_pair(d.z), key_pair(d.w));
-      for (uint32_t e = chunk_ge(w, za) & ~chunk_m8(sh, ch); e; e &= e - 1u) {
+    auto chunk_candidates = [&](const uint4 &w, uint32_t ch) {  // w: keys
+      for (uint32_t e = chunk_ge(w, za) & ~(hist ? chunk_m8(sh, ch) : 0u); e; e &= e - 1u) {
         const uint32_t el = (uint32_t)__builtin_ctz(e);
         put(chunk_key(w, el), ch * 8u + el);
       }
+    };
+    // chunk s1 (most often the only one) from its copy; any other from
+    // registers, in a pass over the slots that waves without one skip
+    if ((sm >> s1) & 1u) chunk_candidates(make_uint4(b0, b1, b2, b3), ch1);
+    const uint64_t rest = sm & ~(1ull << s1);
+    if (__ballot(rest != 0ull)) {
+      static_for<0, NCH>([&](auto S) {
+        constexpr int s = decltype(S)::value;
+        if ((rest >> s) & 1u) chunk_candidates(make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]), (uint32_t)(s * kFT + ft));
+      });
     }
 #pragma unroll
     for (int q = 0; q < kMemPer; ++q) {
@@ -914,10 +929,36 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     __syncthreads();
     const uint32_t ncand = uniform(ctr[1]);
     if (ncand > (uint32_t)kGatherCap) return false;
+    if (ncand <= 64u) {
+      // Rank sort: wave w counts, for every candidate i, the candidates
+      // 8w .. 8w + 7 smaller than it; wave 0 adds the eight counts and moves
+      // candidate i to lane rank(i).
+      uint32_t *part = sh.rank_scratch();  // the bitmap is dead
+      const uint32_t i = (uint32_t)tid & 63u, j0 = ((uint32_t)tid >> 6) * 8u;
+      uint32_t p = 0u;
+      if (i < ncand) {
+        const uint64_t g = ss.gather[i];
+#pragma unroll
+        for (uint32_t j = j0; j < j0 + 8u; ++j) p += (j < ncand && ss.gather[j] < g) ? 1u : 0u;
+      }
+      part[tid] = p;
+      __syncthreads();
+      if (tid < 64) {
+        uint32_t rank = 0u;
+#pragma unroll
+        for (int w8 = 0; w8 < kFW; ++w8) rank += part[w8 * 64 + tid];
+        const uint64_t g = (uint32_t)tid < ncand ? ss.gather[tid] : ~0ull;
+        if ((uint32_t)tid >= ncand) rank = (uint32_t)tid;
+        const uint32_t lo32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)g);
+        const uint32_t hi32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)(g >> 32));
+        finish_wave<TR>(((uint64_t)hi32 << 32) | lo32, c, a, r, K, K == 1u);
+      }
+      return true;
+    }
     if (ncand <= (uint32_t)kFT) {
       // Rank sort: candidate i moves to position (number of smaller
       // candidates) when that is below 64; wave 0 finishes the first K.
-      uint64_t *sorted = (uint64_t *)sh.dump_keys();
+      uint64_t *sorted = (uint64_t *)sh.rank_scratch();  // the bitmap is dead
       if ((uint32_t)tid < ncand) {
         const uint64_t g = ss.gather[tid];
         uint32_t rank = 0u;
@@ -937,7 +978,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   if (k_on && c.top_k <= kGatherCap) {  // ---- mid k -------------------------------
     const uint32_t K = (uint32_t)c.top_k;
     uint32_t L;
-    if (!kth_value<NCH>(sh, nmem, K, tvhi, &L)) return false;
+    if (!kth_value<NCH>(sh, hist, nmem, K, tvhi, &L)) return false;
     const uint32_t za = group_low(L, c);
     // gather every element with z >= za: (~(y key << 16) << 32 | index).
     // Count first (8-bit masks per candidate chunk, packed four to a word),
@@ -950,7 +991,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
       if (((cm_word(sh, s >> 1) >> ((s & 1) * 16)) & 0xFFFFu) >= za) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) m8 |= (((k[s][e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) >= za ? 1u : 0u) << e;
-        m8 &= ~slot_m8(sh, s);  // members enter by their z key
+        if (hist) m8 &= ~chunk_m8(sh, (uint32_t)(s * kFT + tid));  // members enter by their z key
       }
       masks[s >> 2] = (s & 3) ? (masks[s >> 2] | (m8 << ((s & 3) * 8))) : m8;
       nmine += (uint32_t)__builtin_popcount(m8);
