@@ -825,13 +825,13 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     const bool valid = (s + 1) * kFT <= nchunks || ch < nchunks;
     if (!valid) cmx = 0u;  // padding: no candidates
     const bool top = cmx > mx;  // selects, not branches
-    s1 = top ? (uint32_t)s : s1;
     b0 = top ? k[s][0] : b0;
     b1 = top ? k[s][1] : b1;
     b2 = top ? k[s][2] : b2;
     b3 = top ? k[s][3] : b3;
+    s1 = top ? (uint32_t)s : s1;
     // made here, while the wave waits for memory anyway (left to itself, the
-    // compiler keeps the 32 conditions and selects after the pass)
+    // compiler keeps the conditions and selects after the pass)
     asm volatile("" : "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3), "+v"(s1));
     mx = max(mx, cmx);
     cmw = (s & 1) ? (cmw | (cmx << 16)) : cmx;
@@ -921,10 +921,12 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
         if ((rest >> s) & 1u) chunk_candidates(make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]), (uint32_t)(s * kFT + ft));
       });
     }
+    if (zmem >= za) {  // this thread's members reach za
 #pragma unroll
-    for (int q = 0; q < kMemPer; ++q) {
-      const uint32_t m = (uint32_t)tid + (uint32_t)q * kFT;
-      if (m < nmem && (mkey[m] >> 16) >= za) put(mkey[m] >> 16, midx[m]);
+      for (int q = 0; q < kMemPer; ++q) {
+        const uint32_t m = (uint32_t)tid + (uint32_t)q * kFT;
+        if (m < nmem && (mkey[m] >> 16) >= za) put(mkey[m] >> 16, midx[m]);
+      }
     }
     __syncthreads();
     const uint32_t ncand = uniform(ctr[1]);
