@@ -327,3 +327,52 @@ def test_engine_one_hot_decode_loop():
         row[0, 0, tok] = 100.0
         got.append(s.sample(row.cuda(), got).token_id)
     assert got == [3, 4, 5]
+
+
+def test_small_k_bound_and_candidate_paths():
+    """Rows that take each branch of the small-k path of the bf16 kernel:
+    the coarse second histogram of the thread-value bound (outliers far
+    above the rest), the block rank finish (65..512 candidates) and the
+    sort finish (more than 512: wide ties at the top), candidate chunks
+    beyond a thread's largest one (top values in one thread's slots), and
+    argmax chunks holding history tokens."""
+    W = _wl()
+    rng = np.random.default_rng(77)
+    for V in (128256, 32000):
+        rows, ks, hists, temps = [], [], [], []
+        for case in range(6):
+            for _ in range(6):
+                x = rng.normal(0.0, 1.0, V).astype(np.float32)
+                k, h, t = 50, [], 1.0
+                if case == 0:  # outliers: the top kTvBins keys hold fewer than k thread values
+                    x[rng.choice(V, 5, replace=False)] = 1000.0
+                elif case == 1:  # 100 equal maxima, k = 20: 65..512 candidates
+                    x[rng.choice(V, 100, replace=False)] = 20.0
+                    k = 20
+                elif case == 2:  # 600 equal maxima: more than 512 candidates
+                    x[rng.choice(V, 600, replace=False)] = 20.0
+                    k = 60
+                elif case == 3:  # the top values in one thread's slots (element 8 * (s * 512 + 7) + 3)
+                    idx = [8 * (s * 512 + 7) + 3 for s in range(V // 4096)]
+                    x[idx] = 8.0 + rng.random(len(idx)).astype(np.float32)
+                    k = 10
+                elif case == 4:  # history tokens beside the largest values, with temperature
+                    top = np.argsort(-x)[:200]
+                    h = list((top + rng.integers(-3, 4, 200)).clip(0, V - 1)) + list(rng.integers(0, V, 500))
+                    k, t = 40, 0.7
+                else:  # greedy with a penalised maximum
+                    top = int(np.argmax(x))
+                    h = [top] * 3 + list(rng.integers(0, V, 100))
+                    k = 1
+                rows.append(x)
+                ks.append(k)
+                hists.append(h)
+                temps.append(t)
+        B = len(rows)
+        xx = W.f32_to_bf16_bits(np.stack(rows))
+        w = _mk(xx, k=np.array(ks, np.int32), t=np.array(temps), rep=[1.3] * B, pres=[0.4] * B, freq=[0.2] * B,
+                u=rng.random(B), history=hists)
+        print(f"[case] small-k paths V={V} B={B}", flush=True)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"small-k-paths-{V}", rep)
+        assert_parity(rep, f"small-k-paths-{V}")
