@@ -6,15 +6,15 @@
 // issued loads and keeps them in registers as 16-bit total-order keys of the
 // RAW logits, two per word: the row is read from memory once.
 //
-// History.  The history ids are loaded first.  While the first part of the
-// row streams in, they are marked in an LDS bitmap over the vocab; a rank map
-// (per 32-token word: the number of history tokens before it, and the word)
-// then gives every distinct history token ("member", at most kFastMembers) a
-// dense index in token order, under which its multiplicity is counted.  The
-// load pass meets every member in registers and stores its raw key under its
-// index, so penalties need no gather from memory.  Each member's penalised
-// key z (Repetition then Presence/Frequency, bf16-rounded per op, as the
-// reference's chain of kernels) is computed once from its raw key and count.
+// History.  The history ids are requested first.  Inside the load pass,
+// after slot kHistAt, they are marked in an LDS bitmap over the vocab; the
+// number of marked tokens before each 32-token bitmap word gives every
+// distinct history token ("member", at most kFastMembers) a dense index in
+// token order, under which its multiplicity is counted; each member's raw
+// logit is then requested with one 16-bit load, and kEarly + 1 slots later
+// its penalised key z (Repetition then Presence/Frequency, bf16-rounded per
+// op, as the reference's chain of kernels) is computed.  The bitmap also
+// tells which chunks hold members.
 // Temperature is not applied per element either: y = bf16(fma(z, 1/T, 0)) is
 // monotone in z, so selection runs on z keys and maps only the keys that
 // matter to y; runs of z keys that round to one y form one tie group, whose
@@ -22,14 +22,16 @@
 //
 // Paths after the load pass:
 //   small k  (top_k <= kSmallK, greedy included): every thread holds one
-//            "thread value", the largest key of its chunks without members,
-//            raised to its members' z keys.  The K-th largest thread value L
-//            (a 256-bin LDS histogram) bounds the K-th largest z from below,
-//            each value being a distinct element.  The chunks whose maximum
-//            reaches the start of L's tie group are copied to LDS, their
-//            elements (and members) at or above it become the candidates,
-//            which one wave sorts and finishes in f64 when there are at most
-//            64 of them.
+//            "thread value": its largest chunk maximum when that chunk holds
+//            no member (else none), raised to its members' z keys -- each a
+//            distinct element's key.  The K-th largest thread value L (LDS
+//            histograms) bounds the K-th largest z from below.  Every
+//            element at or above the start of L's tie group is a candidate:
+//            those of the thread's largest chunk, whose keys the load pass
+//            kept, of its other chunks whose maximum reaches the bound (rare;
+//            from registers) and the members.  Up to 64 candidates are
+//            ranked across the waves and finished by one wave in f64; up to
+//            512 ranked by one thread each; more are sorted in LDS.
 //   mid k    (top_k <= kGatherCap): the same bound from the K-th largest
 //            chunk maximum (a cascade of LDS windows), the candidates
 //            gathered from registers and sorted in LDS.
@@ -62,7 +64,6 @@ constexpr int kHistPer = LMRS_MAX_HISTORY / kFT;
 constexpr int kMemPer = kFastMembers / kFT;
 constexpr int kSmallK = 64;         // top_k bound of the thread-value path
 constexpr int kTvBins = 256;        // bins of the thread-value histogram
-constexpr int kDumpCap = 1024;      // chunks the thread-value path copies to LDS
 
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -911,8 +912,9 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
         put(chunk_key(w, el), ch * 8u + el);
       }
     };
-    // chunk s1 (most often the only one) from its copy; any other from
-    // registers, in a pass over the slots that waves without one skip
+    // chunk s1 (most often the only one) from the keys the load pass kept;
+    // any other from registers, in a pass over the slots that waves without
+    // one skip
     if ((sm >> s1) & 1u) chunk_candidates(make_uint4(b0, b1, b2, b3), ch1);
     const uint64_t rest = sm & ~(1ull << s1);
     if (__ballot(rest != 0ull)) {
@@ -1028,7 +1030,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   }
 
   // ---- full: 65536-bin count histogram ------------------------------------------
-  __syncthreads();  // the bitmap, rank map, copy and window views are dead
+  __syncthreads();  // the bitmap, chunk maxima and window views are dead
   uint32_t *h64 = sh.u32(0);
   {
     uint4 *p = (uint4 *)h64;
