@@ -479,8 +479,12 @@ template <class TR>
 __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const lmrs_sample_args &a, int r,
                                             uint32_t k, bool greedy) {
   const uint32_t lane = threadIdx.x & 63u;
-  const bool in = lane < k;
   const float y = TR::value(~(uint32_t)(g >> 32));
+  if (greedy) {  // Greedy: the first sorted candidate, log_prob 0, no distribution (greedy.rs:22-29)
+    if (lane == 0) write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), 0.0f, y, 0);
+    return;
+  }
+  const bool in = lane < k;
   const float M = TR::value(~(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g >> 32), 0));
   const double w = in ? exp((double)(y - M)) : 0.0;
   const double incl = wave_inclusive<OpSum>(w, 0.0);
@@ -489,14 +493,18 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
     if (lane == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
     return;
   }
+  // Cumulative shares use one reciprocal per normaliser: they differ from
+  // the reference's quotients by an ulp or two, far inside the 1e-6 margin
+  // that flags a row as near a boundary.
   uint32_t keep = k;
   int32_t flags = 0;
-  if (c.top_p < 1.0 && !greedy) {  // Greedy applies no nucleus cut (greedy.rs:22-29)
-    const double acc = incl / total;
+  if (c.top_p < 1.0) {
+    const double rtot = 1.0 / total;
+    const double acc = incl * rtot;
     const uint64_t hit = __ballot(in && acc >= c.top_p);
     if (hit) keep = (uint32_t)__builtin_ctzll(hit) + 1u;
     // nucleus margin at the cut, from the lane of entry keep - 1
-    const double prev = (incl - w) / total;
+    const double prev = (incl - w) * rtot;
     double m = c.top_p - prev;
     if (acc >= c.top_p && acc - c.top_p < m) m = acc - c.top_p;
     if (!(acc >= c.top_p)) m = c.top_p - acc;
@@ -511,11 +519,12 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
   const uint64_t pickm = __ballot(lane < keep && target <= incl);
   const uint32_t pick = pickm ? (uint32_t)__builtin_ctzll(pickm) : keep - 1u;  // fallback: last (mod.rs:52-54)
   if (lane == pick) {
-    const double lo = (incl - w) / sum_keep, hi = incl / sum_keep;
+    const double rkeep = 1.0 / sum_keep;
+    const double lo = (incl - w) * rkeep, hi = incl * rkeep;
     double m = 1.0;
     if (pick > 0u && fabs(c.u - lo) < m) m = fabs(c.u - lo);
     if (pick + 1u < keep && fabs(hi - c.u) < m) m = fabs(hi - c.u);
-    write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), (float)log(w / sum_keep), y,
+    write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), (float)log(w * rkeep), y,
               flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
   }
 }
@@ -782,14 +791,15 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   // slot s, so that a wave never waits long on a full memory queue with
   // data at hand.  The member tables are built inside the load pass, after
   // slot kHistAt, while the row streams in; the members' raw logits are
-  // requested right after them and their keys computed kEarly + 1 slots
+  // requested right after them and their keys computed kAhead + 1 slots
   // later.  No path leaves before the load pass consumes the row.
   const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
   const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
   constexpr int kEarly = NCH / 4;     // slots in flight ahead of the one being processed
   constexpr int kHistAt = 2;          // the slot after which the member tables are built
-  constexpr int kKeysAt = kHistAt + kEarly + 1;  // the slot whose wait covers the members' loads
-  static_assert(kKeysAt < NCH, "member keys inside the load pass");
+  constexpr int kAhead = kEarly;      // (a deeper queue from slot kHistAt on measured slower)
+  constexpr int kKeysAt = kHistAt + kAhead + 1;  // the slot whose wait covers the members' loads
+  static_assert(kKeysAt < NCH && kAhead >= kEarly, "member keys inside the load pass");
   auto issue_slot = [&](int s) {
     const int ch = s * kFT + tid;
     return issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
@@ -810,11 +820,19 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   static_for<0, NCH>([&](auto S) {
     constexpr int s = decltype(S)::value;
     const int ch = s * kFT + tid;
-    if constexpr (s + kEarly < NCH) kv[s + kEarly] = issue_slot(s + kEarly);
+    // the last slot requested before slot s is waited for
+    constexpr int dist = s < kHistAt ? kEarly : kAhead;
+    constexpr int last = s + dist < NCH ? s + dist : NCH - 1;
+    if constexpr (s < kHistAt) {
+      if constexpr (s + kEarly < NCH) kv[s + kEarly] = issue_slot(s + kEarly);
+    } else if constexpr (s == kHistAt) {
+      static_for<kHistAt + kEarly, last + 1>([&](auto T) { kv[decltype(T)::value] = issue_slot(decltype(T)::value); });
+    } else {
+      if constexpr (s + kAhead < NCH) kv[s + kAhead] = issue_slot(s + kAhead);
+    }
     // loads issued after slot s's: later slots, and the members' for the
-    // slots issued before them and waited for after them
-    constexpr int younger =
-        (s + kEarly < NCH ? s + kEarly : NCH - 1) - s + (s > kHistAt && s <= kHistAt + kEarly ? kMemPer : 0);
+    // slots requested before them and waited for after them
+    constexpr int younger = last - s + (s > kHistAt && s <= kHistAt + kAhead ? kMemPer : 0);
     wait_loads<younger>(kv[s]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
