@@ -1,0 +1,128 @@
+"""The engine decode-step mirror (lmrs_amd/engine.py): configuration and
+strategy mapping on the CPU (generation.rs:71-98, 352-365); the batched
+decode step and generation loop on the GPU, against the oracle row by row."""
+import numpy as np
+import pytest
+
+from lmrs_amd import engine as E
+from lmrs_amd import sampling as S
+
+
+def test_generation_config_validation_and_default():
+    c = E.GenerationConfig()
+    assert (c.max_tokens, c.temperature, c.top_p, c.top_k) == (128, 1.0, 1.0, None)  # generation.rs:121-130
+    assert E.GenerationConfig(32, 0.8, 0.95, 40).max_tokens == 32  # generation.rs:64-67
+    for bad in (dict(temperature=0.0), dict(temperature=-1.0), dict(top_p=0.0), dict(top_p=1.5), dict(top_p=-0.1)):
+        with pytest.raises(ValueError):
+            E.GenerationConfig(**bad)
+
+
+def test_sampler_for_mapping():
+    assert E.sampler_for(E.GenerationConfig(top_k=40, top_p=0.5)) == E.RowParams(40, 1.0, 1.0, True)  # top_k wins
+    assert E.sampler_for(E.GenerationConfig(top_p=0.9, temperature=0.7)) == E.RowParams(0, 0.9, 0.7, True)
+    assert E.sampler_for(E.GenerationConfig()) == E.RowParams(1, 1.0, 1.0, False)  # Greedy
+    with pytest.raises(S.SamplingError):
+        E.sampler_for(E.GenerationConfig(top_k=0))  # TopK::new(0)
+    with pytest.raises(S.SamplingError):
+        E.sampler_for(E.GenerationConfig(temperature=float("nan")))  # Temperature::new(NaN)
+
+
+@pytest.mark.gpu
+def test_decode_steps_match_the_oracle_row_by_row():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from helpers import compare, run_oracle
+    from lmrs_amd import workloads as W
+
+    S.lib()
+    rng = np.random.default_rng(5)
+    V = 50000
+    configs = [E.GenerationConfig(8, 1.0, 1.0, None), E.GenerationConfig(8, 0.7, 1.0, 20),
+               E.GenerationConfig(8, 1.3, 0.9, None), E.GenerationConfig(8, 1.0, 0.5, 5),
+               E.GenerationConfig(8, 0.5, 1.0, None)]
+    seqs = [E.SequenceState(c, seed=11 + i) for i, c in enumerate(configs)]
+    batch = E.DecodeBatch(seqs)
+    for step in range(3):
+        x = rng.normal(0, 2, (len(seqs), 1, V)).astype(np.float32)
+        bits = W.f32_to_bf16_bits(x.reshape(len(seqs), V))
+        states = [s.rng for s in seqs]
+        # the reference draws one uniform per stochastic row from the Sampler's LCG
+        us = []
+        for s, st in zip(seqs, states):
+            us.append(S.next_unit(st)[0] if s.params.stochastic else 0.0)
+        hist = [list(s.generated) for s in seqs]
+        logits = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda().reshape(len(seqs), 1, V)
+        out = batch.step(logits)
+        off = np.concatenate([[0], np.cumsum([len(h) for h in hist])]).astype(np.int64)
+        ids = np.concatenate([np.asarray(h, np.uint32) for h in hist] + [np.zeros(0, np.uint32)]).astype(np.uint32)
+        B = len(seqs)
+        w = W.Workload("engine", bits, np.ones(B, np.float32), np.zeros(B, np.float32), np.zeros(B, np.float32),
+                       np.array([s.params.temperature for s in seqs]), np.array([s.params.top_k for s in seqs], np.int32),
+                       np.array([s.params.top_p for s in seqs]), np.array(us), off, ids)
+        ref = run_oracle(w)
+        gpu = {"token_id": np.array([o.token_id for o in out], np.uint32),
+               "log_prob": np.array([o.log_prob for o in out], np.float32),
+               "logit": np.array([o.logit for o in out], np.float32), "status": np.zeros(B, np.int32)}
+        rep = compare(gpu, ref)
+        assert rep["token_mismatch"] == 0 and rep["status_mismatch"] == 0 and rep["logit_mismatch"] == 0, rep
+        for s, st in zip(seqs, states):  # the RNG advances only for rows that draw
+            assert s.rng == (S.next_unit(st)[1] if s.params.stochastic else st)
+
+
+@pytest.mark.gpu
+def test_batched_generate_with_script_models():
+    """The ScriptModel of crates/engine/tests/prefill_decode.rs:11-59, three
+    sequences at once: one-hot logits at the last position, EOS handling."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    V = 8
+    scripts = [[3, 4, 5], [1, 7, 2], [6, 6, 6, 6]]
+    calls = [0, 0, 0]
+
+    def model(step, tokens):
+        live = [i for i in range(3) if calls[i] < len(scripts[i]) and not done[i]]
+        rows = []
+        for i, toks in zip(live, tokens):
+            x = torch.zeros(len(toks), V, dtype=torch.bfloat16)
+            x[-1, scripts[i][calls[i]]] = 100.0
+            calls[i] += 1
+            rows.append(x[-1:])
+        return torch.stack(rows).cuda()  # [B, 1, V]
+
+    done = [False, False, False]
+    cfgs = [E.GenerationConfig(3), E.GenerationConfig(5), E.GenerationConfig(2)]
+    seqs = [E.SequenceState(c, eos_token=7) for c in cfgs]
+    batch = E.DecodeBatch(seqs)
+    step = 0
+    while batch.live():
+        live = batch.live()
+        out = batch.step(model(step, [[0]] * len(live)))
+        for i in range(3):
+            done[i] = seqs[i].finished
+        step += 1
+    assert [s.generated for s in seqs] == [[3, 4, 5], [1], [6, 6]]
+
+
+@pytest.mark.gpu
+def test_generate_loop_counts_up():
+    """generate() over a batch: a model whose logits favour (last token + 1)
+    mod V makes each sequence count up from its prompt's last token; the
+    sequence whose count reaches the EOS id stops there."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    V = 16
+
+    def model(step, tokens):
+        x = torch.zeros(len(tokens), 1, V, dtype=torch.bfloat16)
+        for j, toks in enumerate(tokens):
+            x[j, 0, (toks[-1] + 1) % V] = 50.0
+        return x.cuda()
+
+    got = E.generate(model, [[1, 2], [9], [12]], [E.GenerationConfig(4), E.GenerationConfig(3), E.GenerationConfig(6)],
+                     eos_token=14)
+    assert got == [[3, 4, 5, 6], [10, 11, 12], [13]]
