@@ -52,16 +52,20 @@ extern "C" {
 
 /* Per-row status codes written to status[r] (low byte) ... */
 #define LMRS_ROW_OK 0
-#define LMRS_ROW_EMPTY 1        /* vocab == 0: "cannot sample from empty logits" (strategies/greedy.rs:24-26) */
+#define LMRS_ROW_EMPTY 1        /* vocab == 0: "cannot sample from empty logits" (strategies/greedy.rs:24-26),
+                                   or an empty candidate set (strategies/mod.rs:28-30) */
 #define LMRS_ROW_DISTRIBUTION 2 /* non-finite or non-positive weight sum (strategies/mod.rs:39-43) */
 #define LMRS_ROW_PARAM 3        /* a parameter fails its constructor's validation (repetition.rs:57-64,
-                                   presence.rs:61-71, temperature.rs:43-50, top_p.rs:26-31); top_k < 0 */
+                                   presence.rs:61-71, temperature.rs:43-50, top_p.rs:26-31,
+                                   min_p.rs:27-29); top_k < 0 */
 #define LMRS_ROW_HISTORY 4      /* history longer than LMRS_MAX_HISTORY for this row */
 /* ... and flag bits above it. */
 #define LMRS_ROW_NEAR_BOUNDARY 0x100 /* the uniform lies within 1e-6 of a CDF boundary of the chosen
                                         token, or the nucleus cumulative lies within 1e-6 of top_p at
                                         the cut: the reference's f64 summation order may pick a
-                                        neighbouring token here */
+                                        neighbouring token here; or exp() of a logit at the min-p
+                                        cut lies within 1e-12 (relative) of the threshold, where
+                                        the host and device exp may round to opposite sides */
 
 #define LMRS_MAX_VOCAB 262144  /* largest vocab accepted (2^18) */
 #define LMRS_MAX_HISTORY 4096  /* longest per-row history accepted */
@@ -92,6 +96,11 @@ typedef struct lmrs_sample_args {
   const double *uniforms;          /* in [0, 1): the draw's uniform (next_unit of the reference's
                                       LCG, strategies/mod.rs:57-61, or any caller RNG).  Required
                                       unless every row is greedy; NULL reads as 0. */
+  const double *min_p;             /* in [0, 1]: MinP's cut (strategies/min_p.rs:39-55), keeping
+                                      the candidates with exp(f64(l)) >= exp(f64(max)) * min_p;
+                                      negative = off (NULL: off for every row); NaN or > 1 is
+                                      LMRS_ROW_PARAM (min_p.rs:27-29).  A cut that keeps nothing
+                                      is LMRS_ROW_EMPTY. */
 
   /* Outputs (device, length batch).  token_ids is required. */
   uint32_t *token_ids; /* SampleOutput::token_id (sampler/output.rs:14-18) */
@@ -102,7 +111,14 @@ typedef struct lmrs_sample_args {
 
 /* Samples one token per row (the fused replacement of Sampler::sample over a
  * batch).  Asynchronous on `stream`.  Returns LMRS_OK or an LMRS_ERR_* code;
- * per-row problems are reported in status[r] and never fail the call. */
+ * per-row problems are reported in status[r] and never fail the call.
+ *
+ * Per row: the processors, then top_k == 1 is Greedy (no other strategy
+ * parameter applies); otherwise the candidates are cut by top-k (top_k.rs:39-45),
+ * then by min-p (min_p.rs:45-53), then by the nucleus (top_p.rs:45-58), and
+ * softmax_choice draws from what is left (strategies/mod.rs:27-55).  Each cut
+ * that is off keeps everything, so a row with one strategy parameter set is
+ * exactly that reference strategy. */
 int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream);
 
 /* Applies the processor chain only (Repetition -> Presence/Frequency ->

@@ -474,7 +474,10 @@ __device__ __forceinline__ uint32_t member_keys(FastShared &sh, const uint32_t (
 
 // ---- selection over LDS data ------------------------------------------------------
 
-// (top_p.rs:45-58) and softmax_choice (strategies/mod.rs:27-55).
+// Finishes a row from its first k sorted candidates, one per lane of a wave
+// (lane i holds entry i, ((~key) << 32 | index)): the min-p cut
+// (min_p.rs:45-53), the nucleus cut (top_p.rs:45-58) and softmax_choice
+// (strategies/mod.rs:27-55).
 template <class TR>
 __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const lmrs_sample_args &a, int r,
                                             uint32_t k, bool greedy) {
@@ -484,8 +487,20 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
     if (lane == 0) write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), 0.0f, y, 0);
     return;
   }
-  const bool in = lane < k;
   const float M = TR::value(~(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g >> 32), 0));
+  int32_t flags = 0;
+  if (c.min_p >= 0.0) {  // the min-p cut (min_p.rs:45-53): a prefix of the k candidates
+    const double thr = minp_threshold(M, c);
+    const uint32_t kk = (uint32_t)__builtin_popcountll(__ballot(lane < k && minp_keeps(y, thr)));
+    if (kk == 0u) {  // softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (lane == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return;
+    }
+    if (__ballot((lane + 1u == kk || (lane == kk && lane < k)) && minp_near(y, M, thr)))
+      flags |= LMRS_ROW_NEAR_BOUNDARY;
+    k = kk;
+  }
+  const bool in = lane < k;
   const double w = in ? exp((double)(y - M)) : 0.0;
   const double incl = wave_inclusive<OpSum>(w, 0.0);
   const double total = lane63(incl);
@@ -497,7 +512,6 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
   // the reference's quotients by an ulp or two, far inside the 1e-6 margin
   // that flags a row as near a boundary.
   uint32_t keep = k;
-  int32_t flags = 0;
   if (c.top_p < 1.0) {
     const double rtot = 1.0 / total;
     const double acc = incl * rtot;
@@ -1209,6 +1223,41 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     cand_mass = mass_excl(last_h) + (double)last_keep * weight_of(last_h);
   }
   int32_t flags = 0;
+  if (c.min_p >= 0.0) {
+    // the min-p cut (min_p.rs:45-53): the entries with y at or above the
+    // lowest y key it keeps, a prefix of whole tie groups
+    const double thr = minp_threshold(M, c);
+    if (!(thr == thr)) {  // NaN threshold: softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    const uint32_t ymp = minp_low_key(kNegInfKey16, ykey_of(0), thr, [](uint32_t k) { return key16_value(k); });
+    int fm = 0x7FFFFFFF;
+    for (int i = E - 1; i >= 0; --i) {
+      const int e = tid * E + i;
+      if (e < nb && ykey_of(e) < ymp) fm = e;
+    }
+    fm = block_min<kFW>(fm, sh.iscr);
+    if (fm == 0x7FFFFFFF) fm = nb;
+    if (fm == 0) {  // not reached: the maximum always passes a non-NaN threshold
+      if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    if (fm - 1 < last_h) {  // the cut ends above the top-k set's last tie group
+      last_e = fm - 1;
+      last_h = group_head(last_e);
+      last_keep = cincl[last_e] - cnt_excl(last_h);
+      cand_mass = mincl[last_e];
+    }
+    if (minp_near(key16_value(ymp), M, thr) || (ymp > kNegInfKey16 && minp_near(key16_value(ymp - 1u), M, thr)))
+      flags |= LMRS_ROW_NEAR_BOUNDARY;
+  }
+  // softmax_choice's distribution check (strategies/mod.rs:39-43) on the
+  // candidates: a non-finite maximum makes their weights NaN
+  if (!(__builtin_isfinite(cand_mass) && cand_mass > 0.0)) {
+    if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
+    return true;
+  }
   double kept_mass = cand_mass;
   if (c.top_p < 1.0) {
     // nucleus cut (top_p.rs:45-58) over the candidates

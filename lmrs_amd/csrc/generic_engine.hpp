@@ -345,7 +345,8 @@ __device__ __forceinline__ void sort_gather(SelState &ss, uint32_t n) {
 
 // Finishes a row from its sorted candidate list: ss.gather[0..k) holds
 // ((~key) << 32 | index) in ascending order, i.e. the reference's sorted
-// order.  Applies the nucleus cut (top_p.rs:45-58) and softmax_choice
+// order.  Applies the min-p cut (min_p.rs:45-53), the nucleus cut
+// (top_p.rs:45-58) and softmax_choice
 // (strategies/mod.rs:27-55) with f64 weights exp(f64(l - max)) and f64
 // prefix sums, and writes the outputs.
 template <class TR, int NT = kThreads>
@@ -354,6 +355,31 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
   // Thread t owns sorted entries P*t .. P*t+P-1 of the first k.
   constexpr int P = kGatherCap / NT, NW = NT / 64;
   const float M = TR::value(~uniform((uint32_t)(ss.gather[0] >> 32)));
+  int32_t flags = 0;
+  if (c.min_p >= 0.0) {  // the min-p cut (min_p.rs:45-53): a prefix of the k candidates
+    const double thr = minp_threshold(M, c);
+    uint32_t nk = 0u;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
+      if (i < k && minp_keeps(TR::value(~(uint32_t)(ss.gather[i] >> 32)), thr)) ++nk;
+    }
+    nk = block_sum<NW>(nk, ss.uscr);
+    if (nk == 0u) {  // softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (threadIdx.x == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return;
+    }
+    int32_t near = 0;
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const uint32_t i = (uint32_t)P * threadIdx.x + (uint32_t)q;
+      if ((i + 1u == nk || (i == nk && i < k)) &&
+          minp_near(TR::value(~(uint32_t)(ss.gather[i] >> 32)), M, thr))
+        near = 1;
+    }
+    if (block_max<NW>(near, ss.iscr)) flags |= LMRS_ROW_NEAR_BOUNDARY;
+    k = nk;
+  }
   double wv[P], incl[P], local = 0.0;
 #pragma unroll
   for (int q = 0; q < P; ++q) {
@@ -375,7 +401,6 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
     return;
   }
   uint32_t keep = k;
-  int32_t flags = 0;
   if (c.top_p < 1.0) {
     int first = 0x7FFFFFFF;
 #pragma unroll
@@ -451,7 +476,7 @@ __device__ __forceinline__ void finish_small_k(SelState &ss, const Row &row, con
 }
 
 // The whole selection for one row from any row source: greedy, top-k,
-// nucleus cut and draw.  kmax/imax/nneg come from the caller's stats pass.
+// min-p cut, nucleus cut and draw.  kmax/imax/nneg come from the caller's stats pass.
 template <class Row>
 __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const RowCfg &c,
                                            const lmrs_sample_args &a, int r, int64_t V,
@@ -464,9 +489,25 @@ __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const R
   }
   const bool k_on = c.top_k > 0 && c.top_k < V;
   const uint32_t ncand = k_on ? (uint32_t)c.top_k : (uint32_t)V;
+  // The min-p cut (min_p.rs:45-53) keeps the keys >= key_mp: a NaN threshold
+  // keeps nothing, and negative NaNs (keys below -inf) never pass.
+  const bool mp_on = c.min_p >= 0.0;
+  uint32_t key_mp = 0u;
+  int32_t flags = 0;
+  if (mp_on) {
+    const double thr = minp_threshold(M, c);
+    if (!(thr == thr)) {  // softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (threadIdx.x == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return;
+    }
+    key_mp = minp_low_key(TR::kNegInfKey, kmax, thr, [](uint32_t k) { return TR::value(k); });
+    if (minp_near(TR::value(key_mp), M, thr) ||
+        (key_mp > TR::kNegInfKey && minp_near(TR::value(key_mp - 1u), M, thr)))
+      flags |= LMRS_ROW_NEAR_BOUNDARY;
+  }
   // Weights exp(f64(l - max)) are all finite and the sum positive unless the
   // maximum is non-finite or a (negative) NaN is among the candidates.
-  if (!__builtin_isfinite(M) || (nneg > 0u && ncand > (uint32_t)V - nneg)) {
+  if (!__builtin_isfinite(M) || (!mp_on && nneg > 0u && ncand > (uint32_t)V - nneg)) {
     if (threadIdx.x == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
     return;
   }
@@ -493,7 +534,11 @@ __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const R
   uint32_t kept_low = k_on ? tk : 0u;
   bool kept_clamp = k_on;
   uint32_t kept_ckey = tk, kept_excess = k_on ? neq_k - needed : 0u;
-  int32_t flags = 0;
+  if (mp_on && (!k_on || key_mp > tk)) {  // the min-p cut ends above the top-k set's lowest key
+    kept_low = key_mp;
+    kept_clamp = false;
+    kept_excess = 0u;
+  }
   if (c.top_p < 1.0) {
     const WeightSel p =
         select_by_weight(ss, row, c.top_p, kept_low, kept_clamp, kept_ckey, kept_excess, M);

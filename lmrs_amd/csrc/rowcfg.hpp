@@ -26,6 +26,7 @@ struct RowCfg {
   float scale;         // (float)(1.0 / T)
   int64_t top_k;       // 0 = off
   double top_p;        // >= 1.0 = off
+  double min_p;        // < 0 = off
   double u;
   int64_t h_begin, h_len;
 };
@@ -71,6 +72,7 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
   c.scale = uniform(s.scale);
   c.top_k = uniform(s.top_k);
   c.top_p = uniform(s.top_p);
+  c.min_p = uniform(s.min_p);
   c.u = uniform(s.u);
   c.h_begin = uniform(s.h_begin);
   c.h_len = uniform(s.h_len);
@@ -80,7 +82,8 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
 // Reads and validates row r's parameters (thread 0 only).  Validation
 // mirrors the constructors: RepetitionPenalty::new (repetition.rs:57-64),
 // FrequencyPresencePenalty::new (presence.rs:61-71), Temperature::new
-// (temperature.rs:43-50), TopP::new (top_p.rs:26-31); top_k < 0 invalid.
+// (temperature.rs:43-50), TopP::new (top_p.rs:26-31), MinP::new
+// (min_p.rs:27-29, a negative value switching the cut off); top_k < 0 invalid.
 __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype) {
   RowCfg c;
   c.status = LMRS_ROW_OK;
@@ -90,10 +93,11 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   double t = a.temperature ? a.temperature[r] : 1.0;
   int64_t k = a.top_k ? (int64_t)a.top_k[r] : 0;
   double p = a.top_p ? a.top_p[r] : 1.0;
+  double mp = a.min_p ? a.min_p[r] : -1.0;
   c.u = a.uniforms ? a.uniforms[r] : 0.0;
   if (!(__builtin_isfinite(rep) && rep > 0.0f) || !__builtin_isfinite(pres) ||
       !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < 0 ||
-      !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0))
+      !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0) || __builtin_isnan(mp) || mp > 1.0)
     c.status = LMRS_ROW_PARAM;
   c.h_begin = 0;
   c.h_len = 0;
@@ -121,7 +125,43 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   c.scale = (float)(1.0 / t);                                  // temperature.rs:71
   c.top_k = k;
   c.top_p = p;
+  c.min_p = mp < 0.0 ? -1.0 : mp;
   return c;
+}
+
+// ---- the min-p cut (min_p.rs:45-53) ----------------------------------------------
+// A candidate l is kept when exp(f64(l)) >= exp(f64(max)) * min_p.  exp is
+// monotone, so over the sorted candidates the kept set is a prefix: NaN
+// thresholds keep nothing and negative NaNs, which sort last, always fail.
+
+__device__ __forceinline__ double minp_threshold(float max, const RowCfg &c) {
+  return exp((double)max) * c.min_p;
+}
+
+__device__ __forceinline__ bool minp_keeps(float l, double thr) { return exp((double)l) >= thr; }
+
+// Whether a logit at the cut is too close to the threshold for the host's
+// and the device's exp to agree on its side (each is within an ulp or two of
+// the exact value); logits equal to the maximum compare exp(max) with itself.
+__device__ __forceinline__ bool minp_near(float l, float max, double thr) {
+  if (l == max || __builtin_isnan(l) || !__builtin_isfinite(thr)) return false;
+  const double e = exp((double)l);
+  return fabs(e - thr) <= 1e-12 * thr + 1e-300;
+}
+
+// The lowest key in [lo, hi] whose value the cut keeps, given that it keeps
+// value(hi) (true whenever the threshold is not NaN): a binary search over
+// the total-order keys, which is where the cut lies on any candidate list.
+template <class VF>
+__device__ __forceinline__ uint32_t minp_low_key(uint32_t lo, uint32_t hi, double thr, VF value) {
+  while (lo < hi) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (minp_keeps(value(mid), thr))
+      hi = mid;
+    else
+      lo = mid + 1u;
+  }
+  return hi;
 }
 
 // Builds the history tables for the row (all NT threads; ends with a barrier).

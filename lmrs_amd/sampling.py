@@ -47,6 +47,7 @@ class SampleArgs(ctypes.Structure):
         ("top_k", ctypes.c_void_p),
         ("top_p", ctypes.c_void_p),
         ("uniforms", ctypes.c_void_p),
+        ("min_p", ctypes.c_void_p),
         ("token_ids", ctypes.c_void_p),
         ("log_probs", ctypes.c_void_p),
         ("logits_out", ctypes.c_void_p),
@@ -135,7 +136,7 @@ class PreparedBatch:
 
 def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
                   presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
-                  top_p=None, uniforms=None, out=None) -> PreparedBatch:
+                  top_p=None, uniforms=None, min_p=None, out=None) -> PreparedBatch:
     """Validates the host-side shapes and builds the argument block of
     ``lmrs_sample_fwd`` (per-row parameters as tensors or sequences of length
     B, None = neutral)."""
@@ -156,6 +157,7 @@ def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalt
     tk = _dev_array(top_k, torch.int32, dev)
     tp = _dev_array(top_p, torch.float64, dev)
     uu = _dev_array(uniforms, torch.float64, dev)
+    mp = _dev_array(min_p, torch.float64, dev)
     if out is None:
         out = {
             "token_ids": torch.empty(B, dtype=torch.int32, device=dev),
@@ -164,19 +166,22 @@ def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalt
             "status": torch.empty(B, dtype=torch.int32, device=dev),
         }
     args = SampleArgs(
-        _ptr(logits), dt, B, V, logits.stride(0) if B > 0 else V,
-        _ptr(hist_offsets), _ptr(hist_ids), _ptr(rp), _ptr(pp), _ptr(fp), _ptr(tt), _ptr(tk), _ptr(tp), _ptr(uu),
-        _ptr(out["token_ids"]), _ptr(out["log_probs"]), _ptr(out["logits"]), _ptr(out["status"]),
+        logits=_ptr(logits), dtype=dt, batch=B, vocab=V, row_stride=logits.stride(0) if B > 0 else V,
+        hist_offsets=_ptr(hist_offsets), hist_ids=_ptr(hist_ids), repetition_penalty=_ptr(rp),
+        presence_penalty=_ptr(pp), frequency_penalty=_ptr(fp), temperature=_ptr(tt), top_k=_ptr(tk),
+        top_p=_ptr(tp), uniforms=_ptr(uu), min_p=_ptr(mp), token_ids=_ptr(out["token_ids"]),
+        log_probs=_ptr(out["log_probs"]), logits_out=_ptr(out["logits"]), status=_ptr(out["status"]),
     )
-    return PreparedBatch(args, out, (logits, rp, pp, fp, tt, tk, tp, uu, hist_offsets, hist_ids))
+    return PreparedBatch(args, out, (logits, rp, pp, fp, tt, tk, tp, uu, mp, hist_offsets, hist_ids))
 
 
 def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
                  presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
-                 top_p=None, uniforms=None, stream=None, out=None):
+                 top_p=None, uniforms=None, min_p=None, stream=None, out=None):
     """Samples one token per row of a [B, V] bf16/f32 CUDA tensor.
 
-    Per-row parameters are tensors or sequences of length B (None = neutral).
+    Per-row parameters are tensors or sequences of length B (None = neutral;
+    a negative min_p switches that row's min-p cut off).
     Returns dict(token_ids uint32-as-int32, log_probs f32, logits f32, status i32),
     all on the logits' device; the call is asynchronous on `stream`.
     """
@@ -184,7 +189,7 @@ def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty
     pb = prepare_batch(logits, hist_offsets=hist_offsets, hist_ids=hist_ids,
                        repetition_penalty=repetition_penalty, presence_penalty=presence_penalty,
                        frequency_penalty=frequency_penalty, temperature=temperature, top_k=top_k,
-                       top_p=top_p, uniforms=uniforms, out=out)
+                       top_p=top_p, uniforms=uniforms, min_p=min_p, out=out)
     s = stream if stream is not None else torch.cuda.current_stream(logits.device)
     pb.launch(s)
     out = pb.out
@@ -208,8 +213,10 @@ def process_logits(logits, *, hist_offsets=None, hist_ids=None, repetition_penal
     tt = _dev_array(temperature, torch.float64, dev)
     status = torch.empty(B, dtype=torch.int32, device=dev)
     out = torch.empty((B, V), dtype=logits.dtype, device=dev)
-    args = SampleArgs(_ptr(logits), dt, B, V, logits.stride(0) if B > 0 else V, _ptr(hist_offsets), _ptr(hist_ids),
-                      _ptr(rp), _ptr(pp), _ptr(fp), _ptr(tt), None, None, None, None, None, None, _ptr(status))
+    args = SampleArgs(logits=_ptr(logits), dtype=dt, batch=B, vocab=V, row_stride=logits.stride(0) if B > 0 else V,
+                      hist_offsets=_ptr(hist_offsets), hist_ids=_ptr(hist_ids), repetition_penalty=_ptr(rp),
+                      presence_penalty=_ptr(pp), frequency_penalty=_ptr(fp), temperature=_ptr(tt),
+                      status=_ptr(status))
     s = stream if stream is not None else torch.cuda.current_stream(dev)
     rc = lib().lmrs_process_logits_fwd(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()),
                                        ctypes.c_void_p(s.cuda_stream))
@@ -237,6 +244,7 @@ class SamplingStrategy:
 
     top_k = 0
     top_p = 1.0
+    min_p = -1.0  # off
     stochastic = True
 
 
@@ -277,6 +285,15 @@ class TopP(SamplingStrategy):
             raise SamplingError("top_p must be in (0, 1]")
         self.p = p
         self.top_p = p
+
+
+class MinP(SamplingStrategy):
+    """MinP (strategies/min_p.rs:19-55)."""
+
+    def __init__(self, min_p: float):
+        if not math.isfinite(min_p) or min_p < 0.0 or min_p > 1.0:
+            raise SamplingError("min_p must be in [0, 1]")
+        self.min_p = float(min_p)
 
 
 class Temperature:
@@ -370,7 +387,7 @@ class Sampler:
         if self.strategy.stochastic:
             u, self.rng = next_unit(self.rng)
         res = sample_batch(row, hist_offsets=off, hist_ids=ids, top_k=[self.strategy.top_k],
-                           top_p=[self.strategy.top_p], uniforms=[u], **kw)
+                           top_p=[self.strategy.top_p], min_p=[self.strategy.min_p], uniforms=[u], **kw)
         torch.cuda.current_stream(row.device).synchronize()
         st = int(res["status"][0].item()) & 0xFF
         if st != ROW_OK:

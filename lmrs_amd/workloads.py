@@ -54,6 +54,7 @@ class Workload:
     hist_offsets: Optional[np.ndarray] = None  # int64 [B+1]
     hist_ids: Optional[np.ndarray] = None      # uint32
     notes: dict = field(default_factory=dict)
+    min_p: Optional[np.ndarray] = None         # float64 [B]; None or negative = off
 
     @property
     def batch(self) -> int:
@@ -77,7 +78,8 @@ class Workload:
         """Bytes one step must move: logits once, history ids, per-row params and outputs."""
         esz = 2 if self.dtype == "bf16" else 4
         hist = 0 if self.hist_ids is None else int(self.hist_offsets[-1]) * 4
-        return self.batch * self.vocab * esz + hist + self.batch * 44
+        mp = 0 if self.min_p is None else self.batch * 8
+        return self.batch * self.vocab * esz + hist + self.batch * 44 + mp
 
     def rows(self, rows) -> "Workload":
         rows = np.asarray(rows)
@@ -88,7 +90,8 @@ class Workload:
             ids = np.concatenate(parts).astype(np.uint32) if parts else np.zeros(0, np.uint32)
         return Workload(self.name, self.logits[rows], self.repetition_penalty[rows], self.presence_penalty[rows],
                         self.frequency_penalty[rows], self.temperature[rows], self.top_k[rows], self.top_p[rows],
-                        self.uniforms[rows], off, ids, dict(self.notes))
+                        self.uniforms[rows], off, ids, dict(self.notes),
+                        None if self.min_p is None else self.min_p[rows])
 
 
 def _params(B, rep=1.0, pres=0.0, freq=0.0, t=1.0, k=0, p=1.0):

@@ -394,11 +394,12 @@ int lmrs_oracle_sample_row(const void *logits, int dtype, int64_t n, const uint3
   if (!valid_repetition(pr->repetition_penalty) ||
       !valid_presence(pr->presence_penalty, pr->frequency_penalty) ||
       !valid_temperature(pr->temperature) || pr->top_k < 0 || !isfinite(pr->top_p) ||
-      pr->top_p <= 0.0 || pr->top_p > 1.0)
-    return LMRS_ORACLE_ERR_PARAM;
+      pr->top_p <= 0.0 || pr->top_p > 1.0 || isnan(pr->min_p) || pr->min_p > 1.0)
+    return LMRS_ORACLE_ERR_PARAM; /* min_p: min_p.rs:27-29, negative = off */
   if (diag) {
     diag->cdf_margin = INFINITY;
     diag->top_p_margin = INFINITY;
+    diag->min_p_margin = INFINITY;
     diag->cum_before = 0.0;
     diag->sum_kept = 0.0;
     diag->weight = 0.0;
@@ -432,7 +433,24 @@ int lmrs_oracle_sample_row(const void *logits, int dtype, int64_t n, const uint3
     lmrs_oracle_sorted_indices(v, n, order);
     int64_t cand = (pr->top_k > 0 && pr->top_k < n) ? pr->top_k : n;
     if (diag) diag->n_candidates = cand;
-    if (pr->top_p < 1.0) {
+    if (pr->min_p >= 0.0) {
+      /* MinP's filter (min_p.rs:44-53) over the top-k candidates */
+      float max = v[order[0]];
+      double threshold = exp((double)max) * pr->min_p;
+      double margin = INFINITY;
+      int64_t nk = 0;
+      for (int64_t i = 0; i < cand; ++i) {
+        float l = v[order[i]];
+        double e = exp((double)l);
+        if (l != max && !isnan(l) && isfinite(threshold) && threshold > 0.0 &&
+            fabs(e - threshold) / threshold < margin)
+          margin = fabs(e - threshold) / threshold;
+        if (e >= threshold) order[nk++] = order[i];
+      }
+      if (diag) diag->min_p_margin = margin;
+      cand = nk;
+    }
+    if (cand > 0 && pr->top_p < 1.0) {
       double margin = INFINITY;
       cand = nucleus_keep(v, order, cand, pr->top_p, &margin);
       if (diag) diag->top_p_margin = margin;

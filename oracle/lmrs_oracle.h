@@ -19,8 +19,8 @@
  *   processors ............ reference doctest vectors, exhaustive 65536-input
  *                            sweeps against numpy f32 + torch bf16 arithmetic
  *   composition ........... reduces to each single reference strategy
- *                            (TopK / TopP / Greedy / full draw) when the
- *                            other filter is off
+ *                            (TopK / TopP / MinP / Greedy / full draw) when
+ *                            the other filters are off
  */
 #ifndef LMRS_ORACLE_H
 #define LMRS_ORACLE_H
@@ -97,6 +97,7 @@ typedef struct {
   double temperature;       /* 1.0 = off */
   int64_t top_k;            /* 0 = off */
   double top_p;             /* >= 1.0 = off; must be in (0, 1] */
+  double min_p;             /* < 0 = off; else must be in [0, 1] */
 } lmrs_oracle_params;
 
 /* Diagnostics used to count ambiguous (boundary) rows.
@@ -105,11 +106,14 @@ typedef struct {
  *   chosen token is alone or the interval has no internal boundary).
  * top_p_margin: distance of the nucleus cumulative to p at the cut
  *   (min(acc_keep - p, p - acc_{keep-1})); +inf when top-p is off.
+ * min_p_margin: smallest |exp(l) - threshold| / threshold over the
+ *   candidates at the min-p cut with l != max (+inf when min-p is off).
  * cum_before: sum of kept weights before the chosen token, f64 in order.
  * sum_kept, weight: normaliser and chosen weight (prob = weight / sum_kept). */
 typedef struct {
   double cdf_margin;
   double top_p_margin;
+  double min_p_margin;
   double cum_before;
   double sum_kept;
   double weight;
@@ -118,8 +122,9 @@ typedef struct {
 } lmrs_oracle_diag;
 
 /* The build's composition (Repetition -> Presence/Frequency -> Temperature,
- * then top-k cut, then nucleus cut over the top-k set, then the inverse-CDF
- * draw with the caller's uniform u), built from reference primitives:
+ * then top-k cut, then min-p cut, then nucleus cut over what is left, then
+ * the inverse-CDF draw with the caller's uniform u), built from reference
+ * primitives:
  * processors as in Sampler::sample (sampler.rs:178-186), strategies as in
  * the strategies/ files.  top_k == 1 is Greedy (greedy.rs:22-29).
  * logits: one row, dtype 0 (bf16 bits) or 2 (f32); not modified.

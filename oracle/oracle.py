@@ -30,6 +30,7 @@ class Params(ctypes.Structure):
         ("temperature", ctypes.c_double),
         ("top_k", ctypes.c_int64),
         ("top_p", ctypes.c_double),
+        ("min_p", ctypes.c_double),
     ]
 
 
@@ -37,6 +38,7 @@ class Diag(ctypes.Structure):
     _fields_ = [
         ("cdf_margin", ctypes.c_double),
         ("top_p_margin", ctypes.c_double),
+        ("min_p_margin", ctypes.c_double),
         ("cum_before", ctypes.c_double),
         ("sum_kept", ctypes.c_double),
         ("weight", ctypes.c_double),
@@ -193,8 +195,8 @@ def temperature(x, t):
 # ---- composed sampler -----------------------------------------------------
 
 def make_params(repetition_penalty=1.0, presence_penalty=0.0, frequency_penalty=0.0,
-                temperature=1.0, top_k=0, top_p=1.0) -> Params:
-    return Params(repetition_penalty, presence_penalty, frequency_penalty, temperature, int(top_k), top_p)
+                temperature=1.0, top_k=0, top_p=1.0, min_p=-1.0) -> Params:
+    return Params(repetition_penalty, presence_penalty, frequency_penalty, temperature, int(top_k), top_p, min_p)
 
 
 def sample_row(logits, history, params: Params, u: float, want_processed=False):
@@ -230,6 +232,7 @@ def sample_batch(logits: np.ndarray, hist_offsets, hist_ids, params_list, unifor
         "logit": np.array([o.logit for o in outs], np.float32),
         "cdf_margin": np.array([d.cdf_margin for d in diags]),
         "top_p_margin": np.array([d.top_p_margin for d in diags]),
+        "min_p_margin": np.array([d.min_p_margin for d in diags]),
         "n_candidates": np.array([d.n_candidates for d in diags]),
         "n_kept": np.array([d.n_kept for d in diags]),
         "prob": np.array([d.weight / d.sum_kept if d.sum_kept > 0 else np.nan for d in diags]),

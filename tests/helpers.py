@@ -7,6 +7,7 @@ import os
 import numpy as np
 
 BOUNDARY = 1e-6      # |u - CDF boundary| or |nucleus cumulative - p| below this is ambiguous
+MINP_BOUNDARY = 1e-12  # |exp(l) - threshold| / threshold at the min-p cut below this is ambiguous
 PROB_RTOL = 1e-5     # post-filter probability tolerance (relative)
 
 
@@ -33,7 +34,8 @@ def run_gpu(w, logits=None, off=None, ids=None):
         logits, off, ids = to_device(w)
     res = S.sample_batch(logits, hist_offsets=off, hist_ids=ids, repetition_penalty=w.repetition_penalty,
                          presence_penalty=w.presence_penalty, frequency_penalty=w.frequency_penalty,
-                         temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, uniforms=w.uniforms)
+                         temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, uniforms=w.uniforms,
+                         min_p=w.min_p)
     torch.cuda.synchronize()
     return {
         "token_id": res["token_ids"].cpu().numpy().view(np.uint32),
@@ -48,7 +50,8 @@ def run_oracle(w, threads=None):
 
     params = [O.make_params(float(w.repetition_penalty[r]), float(w.presence_penalty[r]),
                             float(w.frequency_penalty[r]), float(w.temperature[r]), int(w.top_k[r]),
-                            float(w.top_p[r])) for r in range(w.batch)]
+                            float(w.top_p[r]), -1.0 if w.min_p is None else float(w.min_p[r]))
+              for r in range(w.batch)]
     threads = threads or min(16, os.cpu_count() or 1)
     return O.sample_batch(w.logits, w.hist_offsets, w.hist_ids, params, w.uniforms, n_threads=threads)
 
@@ -57,7 +60,8 @@ def compare(gpu, ref):
     """Returns a report dict; asserts nothing."""
     st_gpu = gpu["status"] & 0xFF
     ok = ref["status"] == 0
-    boundary = ok & ((ref["cdf_margin"] < BOUNDARY) | (ref["top_p_margin"] < BOUNDARY))
+    boundary = ok & ((ref["cdf_margin"] < BOUNDARY) | (ref["top_p_margin"] < BOUNDARY)
+                     | (ref["min_p_margin"] < MINP_BOUNDARY))
     same = gpu["token_id"] == ref["token_id"]
     status_mismatch = int(np.sum(st_gpu != ref["status"]))
     mism = ok & ~same & ~boundary

@@ -1,7 +1,8 @@
 """GPU parity tests: the HIP sampler (through its C-ABI) against the CPU oracle.
 
 Bar: token ids identical except rows where the oracle's uniform lies within
-1e-6 of a CDF boundary (or the nucleus cumulative within 1e-6 of top_p),
+1e-6 of a CDF boundary (or the nucleus cumulative within 1e-6 of top_p, or
+exp of a logit at the min-p cut within 1e-12 relative of the threshold),
 which are counted; processed logit of the chosen token bit-identical;
 post-filter probability exp(log_prob) within 1e-5 relative.
 """
@@ -152,7 +153,8 @@ def _mk(logits, **kw):
         ids = np.concatenate([np.asarray(h, np.uint32) for h in hist]).astype(np.uint32)
     return W.Workload("edge", logits, f("rep", 1.0, np.float32), f("pres", 0.0, np.float32),
                       f("freq", 0.0, np.float32), f("t", 1.0, np.float64), f("k", 0, np.int32),
-                      f("p", 1.0, np.float64), f("u", 0.5, np.float64), off, ids)
+                      f("p", 1.0, np.float64), f("u", 0.5, np.float64), off, ids,
+                      min_p=f("mp", -1.0, np.float64) if "mp" in kw else None)
 
 
 def test_ties_and_small_rows():
@@ -376,3 +378,72 @@ def test_small_k_bound_and_candidate_paths():
         rep = compare(run_gpu(w), run_oracle(w))
         _report(f"small-k-paths-{V}", rep)
         assert_parity(rep, f"small-k-paths-{V}")
+
+
+def test_min_p_on_every_path():
+    """MinP (min_p.rs:39-55) alone and after top-k, before top-p, on every
+    selection path: the bf16 kernel's small-k (wave finish), mid-k (sorted
+    finish) and full-histogram paths, and the generic engine (bf16 rows of
+    odd vocab, f32 rows) with its gathered and weighted paths; plus the
+    threshold's overflow, underflow and NaN cases."""
+    W = _wl()
+    rng = np.random.default_rng(91)
+    # (top_k, top_p, min_p): cut combinations
+    combos = [(0, 1.0, 0.1), (0, 1.0, 0.01), (0, 1.0, 1e-4), (0, 1.0, 0.0), (0, 1.0, 1.0), (0, 0.9, 0.05),
+              (20, 1.0, 0.3), (64, 0.8, 0.02), (50, 1.0, 1e-6), (1000, 1.0, 0.01), (1000, 0.95, 1e-4),
+              (5000, 1.0, 0.001), (5000, 1.0, 0.2), (2, 1.0, 0.9), (0, 1.0, -1.0), (1, 1.0, 0.5)]
+    for dtype, V in (("bf16", 128256), ("bf16", 32001), ("f32", 32000)):
+        rows, ks, ps, mps, hists, temps = [], [], [], [], [], []
+        for i, (k, p, mp) in enumerate(combos):
+            for j in range(2):
+                # normal rows keep thousands of candidates at small min_p, heavy-tailed rows a few
+                x = (rng.normal(0.0, 1.0, V) if j == 0 else rng.standard_t(4, V) * 2.0).astype(np.float32)
+                h, t = [], 1.0
+                if j == 1:  # penalties over a history near the top, with temperature
+                    top = np.argsort(-x)[:100]
+                    h = list(top[::3]) + list(rng.integers(0, V, 300))
+                    t = 0.7
+                rows.append(x)
+                ks.append(k)
+                ps.append(p)
+                mps.append(mp)
+                hists.append(h)
+                temps.append(t)
+        # threshold special cases (no history)
+        specials = []
+        x = rng.normal(0, 1, V).astype(np.float32)
+        x[5], x[9] = 800.0, 750.0            # exp overflows: min_p > 0 keeps l >= ~709.8
+        specials.append((x, 0, 0.5))
+        specials.append((x.copy(), 0, 0.0))  # inf * 0: NaN threshold, empty
+        specials.append((x.copy(), 30, 0.5))
+        specials.append((x - 2000.0, 0, 0.5))  # exp(max) underflows: everything is kept
+        specials.append((x - 2000.0, 40, 0.9))
+        y = rng.normal(0, 1, V).astype(np.float32)
+        y[77] = np.inf
+        specials.append((y, 0, 0.3))          # inf threshold: NaN weights
+        specials.append((y.copy(), 0, 0.0))   # NaN threshold
+        specials.append((y.copy(), 0, -1.0))  # no min-p: invalid distribution
+        specials.append((y.copy(), 5000, -1.0))
+        z = rng.normal(0, 1, V).astype(np.float32)
+        z[3] = np.nan
+        specials.append((z, 0, 0.2))          # NaN maximum: NaN threshold
+        for x, k, mp in specials:
+            rows.append(x)
+            ks.append(k)
+            ps.append(1.0)
+            mps.append(mp)
+            hists.append([])
+            temps.append(1.0)
+        B = len(rows)
+        xx = np.stack(rows)
+        if dtype == "bf16":
+            xx = W.f32_to_bf16_bits(xx)
+        w = _mk(xx, k=np.array(ks, np.int32), p=np.array(ps), mp=np.array(mps), t=np.array(temps),
+                rep=[1.2] * B, pres=[0.3] * B, freq=[0.1] * B, u=rng.random(B), history=hists)
+        print(f"[case] min-p paths {dtype} V={V} B={B}", flush=True)
+        g, r = run_gpu(w), run_oracle(w)
+        rep = compare(g, r)
+        _report(f"min-p-{dtype}-{V}", rep)
+        assert_parity(rep, f"min-p-{dtype}-{V}")
+        st = list(r["status"][-len(specials):])
+        assert st == [0, 1, 0, 0, 0, 2, 1, 2, 2, 1], st

@@ -295,11 +295,93 @@ def test_composition_reduces_to_reference_strategies():
         assert O.sample_row(x, None, O.make_params(top_k=k), u)[1] == a
         _, b, _ = O.top_p(x, p, seed)
         assert O.sample_row(x, None, O.make_params(top_p=p), u)[1] == b
+        mp = float(rng.choice([0.0, 0.02, 0.3, 1.0, rng.uniform(0.0, 1.0)]))
+        st_m, m, _ = O.min_p(x, mp, seed)
+        r = O.sample_row(x, None, O.make_params(min_p=mp), u)
+        assert r[0] == st_m and r[1] == m
         _, g = O.greedy(x)
         assert O.sample_row(x, None, O.make_params(top_k=1), u)[1] == g
         # no filter: full multinomial == TopK(n)
         _, f, _ = O.top_k(x, n, seed)
         assert O.sample_row(x, None, O.make_params(), u)[1] == f
+
+
+def test_reference_min_p_vector_through_composition():
+    # min_p.rs:9-18: MinP(0.1) on [0, 10, 9] with rng 3 picks 1 or 2; the
+    # composed sampler with only min-p on is that strategy
+    for v in VEC["min_p"]:
+        u, _ = O.next_unit(v["rng"])
+        st, out, diag, _ = O.sample_row(np.asarray(v["logits"], np.float32), None,
+                                        O.make_params(min_p=v["min_p"]), u)
+        assert st == O.OK and out[0] in v["token_in"]
+        assert out == O.min_p(v["logits"], v["min_p"], v["rng"])[1]
+        assert diag.n_kept == 2  # exp(9) >= 0.1 * exp(10) keeps 9; exp(0) does not
+
+
+def test_min_p_cut_bruteforce():
+    # min_p strictly between two consecutive ratios exp(l - max) of distinct
+    # values, so the kept set is {l : exp(l - max) >= min_p} whatever exp's
+    # last-bit rounding; draws at interval midpoints of the kept prefix
+    rng = np.random.default_rng(7)
+    for _ in range(80):
+        n = int(rng.integers(2, 10))
+        x = rng.choice(np.arange(-6, 3, dtype=np.float32) / 2, size=n)
+        full = sorted(range(n), key=lambda i: (-x[i], i))
+        m = x[full[0]]
+        ratios = sorted({math.exp(float(x[i] - m)) for i in range(n)}, reverse=True)
+        j = int(rng.integers(0, len(ratios)))
+        lo = ratios[j + 1] if j + 1 < len(ratios) else 0.0
+        mp = math.sqrt(ratios[j] * lo) if lo > 0 else ratios[j] / 2
+        order = [i for i in full if math.exp(float(x[i] - m)) >= ratios[j]]
+        for u in _midpoints(x, order):
+            st, (tok, lp, _), diag, _ = O.sample_row(x, None, O.make_params(min_p=mp), float(u))
+            want, prob = _expected_draw(x, order, u)
+            assert st == O.OK and tok == want and diag.n_kept == len(order)
+            assert math.isclose(math.exp(lp), prob, rel_tol=1e-6)
+        # with a top-k cut first the kept set is the shorter of the two prefixes
+        k = int(rng.integers(1, n + 1))
+        if k > 1:
+            order_k = order[:k]
+            for u in _midpoints(x, order_k):
+                st, (tok, _, _), diag, _ = O.sample_row(x, None, O.make_params(top_k=k, min_p=mp), float(u))
+                assert st == O.OK and tok == _expected_draw(x, order_k, u)[0]
+
+
+def test_min_p_special_values_and_validation():
+    f = lambda *v: np.array(v, np.float32)  # noqa: E731
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    P = O.make_params
+    # NaN maximum: NaN threshold keeps nothing (an empty candidate set)
+    assert O.sample_row(f(1.0, np.nan, 0.5), None, P(min_p=0.1), 0.3)[0] == O.ERR_EMPTY
+    # +inf maximum: inf threshold keeps the overflowing logits, whose weights are NaN
+    assert O.sample_row(f(1.0, np.inf, 0.5), None, P(min_p=0.1), 0.3)[0] == O.ERR_DISTRIBUTION
+    assert O.sample_row(f(1.0, np.inf, 0.5), None, P(min_p=0.0), 0.3)[0] == O.ERR_EMPTY  # inf * 0
+    # exp(800) overflows: min_p 0 gives a NaN threshold, min_p > 0 keeps only l >= ~709.8
+    assert O.sample_row(f(800.0, 0.0, 750.0), None, P(min_p=0.0), 0.3)[0] == O.ERR_EMPTY
+    st, out, diag, _ = O.sample_row(f(800.0, 0.0, 750.0, 700.0), None, P(min_p=0.5), 0.99)
+    assert st == O.OK and diag.n_kept == 2 and out[0] == 0
+    # exp(max) underflows to 0: every non-NaN logit is kept
+    st, out, diag, _ = O.sample_row(f(-800.0, -801.0), None, P(min_p=0.5), 0.99)
+    assert st == O.OK and diag.n_kept == 2 and out[0] == 1
+    # a negative NaN sorts last and never passes, so min-p rescues the row
+    row = f(1.0, 0.0, 0.5)
+    row[1] = neg_nan
+    assert O.sample_row(row, None, P(), 0.3)[0] == O.ERR_DISTRIBUTION
+    st, out, diag, _ = O.sample_row(row, None, P(min_p=0.0), 0.99)
+    assert st == O.OK and diag.n_kept == 2 and out[0] == 2
+    # min_p 1 keeps the maximum's ties; min_p 0 keeps -inf (weight 0)
+    assert O.sample_row(f(2.0, 2.0, 1.0), None, P(min_p=1.0), 0.3)[1][0] == 0
+    assert O.sample_row(f(2.0, 2.0, 1.0), None, P(min_p=1.0), 0.7)[1][0] == 1
+    r0 = O.sample_row(f(-np.inf, 1.0, 0.0), None, P(min_p=0.0), 0.9)
+    assert r0[2].n_kept == 3 and r0[1] == O.sample_row(f(-np.inf, 1.0, 0.0), None, P(), 0.9)[1]
+    assert O.sample_row(f(-np.inf, -np.inf), None, P(min_p=0.5), 0.3)[0] == O.ERR_DISTRIBUTION
+    # validation (min_p.rs:27-29); negative is off
+    assert O.sample_row(f(1.0, 0.0), None, P(min_p=float("nan")), 0.3)[0] == O.ERR_PARAM
+    assert O.sample_row(f(1.0, 0.0), None, P(min_p=1.5), 0.3)[0] == O.ERR_PARAM
+    for off in (-0.5, -np.inf):
+        assert O.sample_row(f(1.0, 0.0), None, P(min_p=off), 0.6)[1] == O.sample_row(f(1.0, 0.0), None, P(), 0.6)[1]
+    # greedy ignores min-p
+    assert O.sample_row(f(1.0, np.nan), None, P(top_k=1, min_p=0.5), 0.3)[1][0] == 1
 
 
 def test_top_k_one_is_greedy_and_k_ge_v_is_full():
