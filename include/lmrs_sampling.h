@@ -10,8 +10,8 @@
  * logits/temperature.rs:66-72, each a chain of CUDA elementwise kernels bound
  * through crates/kernels/src/tensor_ops.rs:28-34,142-174), the cast and copy
  * to the host (tensor_ops.rs:176-186), and the host strategy (Greedy / TopK /
- * TopP / softmax_choice, crates/sampling/src/strategies/mod.rs:21-61,
- * greedy.rs:22-29, top_k.rs:39-45, top_p.rs:39-61).
+ * TopP / MinP / softmax_choice, crates/sampling/src/strategies/mod.rs:21-61,
+ * greedy.rs:22-29, top_k.rs:39-45, top_p.rs:39-61, min_p.rs:39-55).
  *
  * Conventions follow the reference's native layer (kernels/ffi, declared in
  * crates/kernels/src/raw.rs:53-147): plain pointers and sizes, dtype codes
@@ -129,6 +129,13 @@ int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream);
  * batch, vocab, row_stride, history and the three penalty / temperature
  * arrays; ignores the rest. */
 int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, void *stream);
+
+/* Device workspace, in bytes, that lmrs_sample_fwd needs for a call of this
+ * shape: always 0.  Every working set (history tables, candidate lists,
+ * histograms) lives in the workgroup's LDS and registers, so the caller
+ * passes no workspace and no call allocates.  Kept so that a caller written
+ * against a workspace-taking sampler (query, allocate, pass) binds unchanged. */
+size_t lmrs_sample_workspace_size(int32_t batch, int64_t vocab, int32_t dtype, int64_t max_hist);
 
 /* Library version string. */
 const char *lmrs_sampling_version(void);

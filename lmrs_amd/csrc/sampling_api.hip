@@ -67,4 +67,6 @@ extern "C" int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, 
   return hipGetLastError() == hipSuccess ? LMRS_OK : LMRS_ERR_LAUNCH;
 }
 
+extern "C" size_t lmrs_sample_workspace_size(int32_t, int64_t, int32_t, int64_t) { return 0; }
+
 extern "C" const char *lmrs_sampling_version(void) { return "lmrs-mi355x-sampling 0.2 (gfx950)"; }

@@ -17,8 +17,12 @@ The per-row semantics are those of the reference's single-row calls:
 """
 from __future__ import annotations
 
+import enum
 from dataclasses import dataclass, field
-from typing import Callable, List, Optional, Sequence
+from collections.abc import Sequence as Seq
+from typing import Callable, List, Optional
+
+import numpy as np
 
 from . import sampling as S
 
@@ -101,7 +105,7 @@ class SequenceState:
 class DecodeBatch:
     """Samples the next token of every live sequence with one launch."""
 
-    def __init__(self, sequences: Sequence[SequenceState]):
+    def __init__(self, sequences: Seq[SequenceState]):
         self.sequences = list(sequences)
 
     def live(self) -> List[int]:
@@ -154,8 +158,8 @@ class DecodeBatch:
         return out
 
 
-def generate(model: Callable, prompts: Sequence[Sequence[int]], configs: Sequence[GenerationConfig],
-             eos_token: Optional[int] = None, seeds: Optional[Sequence[int]] = None) -> List[List[int]]:
+def generate(model: Callable, prompts: Seq[Seq[int]], configs: Seq[GenerationConfig],
+             eos_token: Optional[int] = None, seeds: Optional[Seq[int]] = None) -> List[List[int]]:
     """GenerationEngine::generate (generation.rs:308-346) for a batch of
     prompts: `model(step, tokens)` receives, for each live sequence in order,
     the tokens to run (the whole prompt at step 0, then its last token) and
@@ -181,3 +185,178 @@ def generate(model: Callable, prompts: Sequence[Sequence[int]], configs: Sequenc
         if step > max((c.max_tokens for c in configs), default=0) + 1:
             break
     return [s.generated for s in seqs]
+
+
+# ---------------------------------------------------------------------------
+# the wire format and the scheduler's side of a sample
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class GenerateParams:
+    """GenerateParams (crates/server/src/types/openai.rs:101-158): the
+    normalised request; temperature and top_p travel as f32 (defaults
+    128 / 1.0 / 1.0 / None / no stop strings, :153-157)."""
+
+    max_tokens: int = 128
+    temperature: float = 1.0
+    top_p: float = 1.0
+    top_k: Optional[int] = None
+    stop: tuple = ()
+
+    def __post_init__(self):
+        object.__setattr__(self, "temperature", float(np.float32(self.temperature)))
+        object.__setattr__(self, "top_p", float(np.float32(self.top_p)))
+
+    @classmethod
+    def from_request(cls, req: dict) -> "GenerateParams":
+        """From a completion or chat request's optional fields (openai.rs:160-182)."""
+        return cls(req.get("max_tokens") or 128,
+                   1.0 if req.get("temperature") is None else req["temperature"],
+                   1.0 if req.get("top_p") is None else req["top_p"],
+                   req.get("top_k"), tuple(req.get("stop") or ()))
+
+    def to_generation_config(self) -> GenerationConfig:
+        """ServerEngine::generate (crates/server/src/engine.rs:115-122): the f32
+        values widened to f64, so T = 0.7 arrives as 0.699999988079071."""
+        return GenerationConfig(self.max_tokens, float(self.temperature), float(self.top_p), self.top_k)
+
+
+class FinishReason(enum.Enum):
+    """FinishReason (crates/engine/src/sequence/status.rs:12-31)."""
+
+    EOS = "eos"
+    LENGTH = "length"
+    STOPPED = "stopped"
+
+    def __str__(self) -> str:
+        return self.value
+
+
+class SequenceStatus(enum.Enum):
+    """SequenceStatus (status.rs:47-74)."""
+
+    WAITING = "waiting"
+    RUNNING = "running"
+    SWAPPED = "swapped"
+    FINISHED = "finished"
+    ABORTED = "aborted"
+
+    def can_prefill(self) -> bool:
+        return self is SequenceStatus.WAITING
+
+    def is_runnable(self) -> bool:
+        return self in (SequenceStatus.WAITING, SequenceStatus.RUNNING)
+
+    def is_terminal(self) -> bool:
+        return self in (SequenceStatus.FINISHED, SequenceStatus.ABORTED)
+
+
+class SequenceError(RuntimeError):
+    """SequenceError (crates/engine/src/sequence/sequence.rs:8-27)."""
+
+
+_TRANSITIONS = {
+    (SequenceStatus.WAITING, SequenceStatus.RUNNING), (SequenceStatus.WAITING, SequenceStatus.FINISHED),
+    (SequenceStatus.WAITING, SequenceStatus.ABORTED), (SequenceStatus.RUNNING, SequenceStatus.SWAPPED),
+    (SequenceStatus.RUNNING, SequenceStatus.FINISHED), (SequenceStatus.RUNNING, SequenceStatus.ABORTED),
+    (SequenceStatus.SWAPPED, SequenceStatus.RUNNING), (SequenceStatus.SWAPPED, SequenceStatus.ABORTED),
+}
+
+
+def validate_transition(src: SequenceStatus, dst: SequenceStatus) -> None:
+    """validate_transition (status.rs:98-118)."""
+    if src != dst and (src, dst) not in _TRANSITIONS:
+        raise SequenceError(f"invalid sequence status transition from {src} to {dst}")
+
+
+class Sequence:
+    """Sequence (sequence.rs:48-213): the token buffer and lifecycle of one
+    request, which receives each SampleOutput through append_sample."""
+
+    def __init__(self, seq_id: int, prompt_tokens: Seq[int], max_new_tokens: int,
+                 eos_token: Optional[int] = None):
+        if len(prompt_tokens) == 0:
+            raise SequenceError("sequence prompt cannot be empty")
+        self.id = seq_id
+        self.prompt_tokens = list(prompt_tokens)
+        self.generated: List[S.SampleOutput] = []
+        self.max_new_tokens = max_new_tokens
+        self.eos_token = eos_token
+        self.processed_len = 0
+        self.status = SequenceStatus.WAITING
+        self.finish_reason: Optional[FinishReason] = None
+
+    def generated_token_ids(self) -> List[int]:
+        return [o.token_id for o in self.generated]
+
+    def total_len(self) -> int:
+        return len(self.prompt_tokens) + len(self.generated)
+
+    def pending_tokens(self) -> List[int]:
+        return (self.prompt_tokens + self.generated_token_ids())[self.processed_len:self.total_len()]
+
+    def has_pending_model_input(self) -> bool:
+        return self.status.is_runnable() and self.processed_len < self.total_len()
+
+    def _set_status(self, status: SequenceStatus) -> None:
+        validate_transition(self.status, status)
+        self.status = status
+
+    def mark_processed(self, token_count: int) -> None:
+        """sequence.rs:143-158."""
+        processed = self.processed_len + token_count
+        if processed > self.total_len():
+            raise SequenceError(f"processed token count {processed} exceeds total token count {self.total_len()}")
+        self.processed_len = processed
+        if self.status is SequenceStatus.WAITING:
+            self._set_status(SequenceStatus.RUNNING)
+
+    def append_sample(self, sample: S.SampleOutput) -> None:
+        """append_sample (sequence.rs:160-172): the sample is kept, EOS included;
+        EOS finishes with Eos, reaching max_new_tokens with Length."""
+        if self.status.is_terminal():
+            raise SequenceError(f"sequence {self.id} is terminal")
+        self.generated.append(sample)
+        if self.eos_token is not None and sample.token_id == self.eos_token:
+            self._finish(FinishReason.EOS)
+        elif len(self.generated) >= self.max_new_tokens:
+            self._finish(FinishReason.LENGTH)
+
+    def stop(self) -> None:
+        self._finish(FinishReason.STOPPED)
+
+    def abort(self) -> None:
+        self.finish_reason = None
+        self._set_status(SequenceStatus.ABORTED)
+
+    def swap_out(self) -> None:
+        self._set_status(SequenceStatus.SWAPPED)
+
+    def resume(self) -> None:
+        self._set_status(SequenceStatus.RUNNING)
+
+    def _finish(self, reason: FinishReason) -> None:
+        self.finish_reason = reason
+        self._set_status(SequenceStatus.FINISHED)
+
+
+@dataclass(frozen=True)
+class StepOutput:
+    """StepOutput (crates/engine/src/executor/output.rs:16-44)."""
+
+    sequence_id: int
+    sample: S.SampleOutput
+
+
+def run_batch(sampler: S.Sampler, logits, sequence_ids: Seq[int]) -> List[StepOutput]:
+    """Worker::run_batch (crates/engine/src/worker/worker.rs:137-157) after the
+    model: one launch samples the last-token logits of every entry with the
+    worker's one Sampler and an empty history, as the reference's entry loop
+    does, and pairs each sample with its sequence id."""
+    rows = last_token_logits(logits)
+    if rows.shape[0] != len(sequence_ids):
+        raise ValueError(f"{rows.shape[0]} logits rows for {len(sequence_ids)} entries")
+    if rows.shape[0] == 0:
+        return []
+    samples = sampler.sample_rows(rows.contiguous())
+    return [StepOutput(i, o) for i, o in zip(sequence_ids, samples)]

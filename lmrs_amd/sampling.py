@@ -73,6 +73,8 @@ def lib():
         L.lmrs_sample_fwd.restype = ctypes.c_int
         L.lmrs_process_logits_fwd.argtypes = [ctypes.POINTER(SampleArgs), ctypes.c_void_p, ctypes.c_void_p]
         L.lmrs_process_logits_fwd.restype = ctypes.c_int
+        L.lmrs_sample_workspace_size.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64]
+        L.lmrs_sample_workspace_size.restype = ctypes.c_size_t
         L.lmrs_sampling_version.argtypes = []
         L.lmrs_sampling_version.restype = ctypes.c_char_p
         _lib = L
@@ -369,32 +371,57 @@ class Sampler:
     def processor_count(self) -> int:
         return len(self.processors)
 
-    def sample(self, logits, history: Sequence[int] = ()) -> SampleOutput:
-        """One row (any shape, flattened), like Sampler::sample."""
-        torch = _torch()
-        row = logits.reshape(1, -1)
+    def _processor_kw(self, rows: int) -> dict:
         kw = {}
         for p in self.processors:
             if isinstance(p, RepetitionPenalty):
-                kw["repetition_penalty"] = [p.penalty]
+                kw["repetition_penalty"] = [p.penalty] * rows
             elif isinstance(p, FrequencyPresencePenalty):
-                kw["presence_penalty"] = [p.presence]
-                kw["frequency_penalty"] = [p.frequency]
+                kw["presence_penalty"] = [p.presence] * rows
+                kw["frequency_penalty"] = [p.frequency] * rows
             elif isinstance(p, Temperature):
-                kw["temperature"] = [p.value]
-        off, ids = history_csr([list(history)], row.device)
-        u, saved = 0.0, self.rng
-        if self.strategy.stochastic:
-            u, self.rng = next_unit(self.rng)
-        res = sample_batch(row, hist_offsets=off, hist_ids=ids, top_k=[self.strategy.top_k],
-                           top_p=[self.strategy.top_p], min_p=[self.strategy.min_p], uniforms=[u], **kw)
-        torch.cuda.current_stream(row.device).synchronize()
-        st = int(res["status"][0].item()) & 0xFF
-        if st != ROW_OK:
-            self.rng = saved  # the reference draws only after validation (strategies/mod.rs:39-44)
-            raise SamplingError({ROW_EMPTY: "cannot sample from empty logits",
-                                 ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
-                                 ROW_PARAM: "invalid sampling parameter",
-                                 ROW_HISTORY: "history too long"}.get(st, f"status {st}"))
-        return SampleOutput(int(res["token_ids"][0].item()) & 0xFFFFFFFF, float(res["log_probs"][0].item()),
-                            float(res["logits"][0].item()))
+                kw["temperature"] = [p.value] * rows
+        return kw
+
+    def sample(self, logits, history: Sequence[int] = ()) -> SampleOutput:
+        """One row (any shape, flattened), like Sampler::sample."""
+        return self.sample_rows(logits.reshape(1, -1), [history])[0]
+
+    def sample_rows(self, rows, histories: Optional[Sequence[Sequence[int]]] = None) -> list:
+        """Sampler::sample on each row of a [B, V] tensor in order, as one
+        launch: the rows share this sampler's processors and strategy, and
+        the stochastic ones draw their uniforms from its one LCG in row order,
+        as B successive calls would (the reference worker samples its batch
+        entries this way, worker.rs:137-157).  On a failing row the error is
+        raised and the LCG is left as the reference leaves it: advanced by the
+        rows before it only, since a row draws after its validation
+        (strategies/mod.rs:39-44)."""
+        torch = _torch()
+        B = rows.shape[0]
+        hist = [list(h) for h in histories] if histories is not None else [[] for _ in range(B)]
+        off, ids = history_csr(hist, rows.device)
+        us, states = [], [self.rng]
+        for _ in range(B):
+            u = 0.0
+            if self.strategy.stochastic:
+                u, self.rng = next_unit(self.rng)
+            us.append(u)
+            states.append(self.rng)
+        res = sample_batch(rows, hist_offsets=off, hist_ids=ids, top_k=[self.strategy.top_k] * B,
+                           top_p=[self.strategy.top_p] * B, min_p=[self.strategy.min_p] * B, uniforms=us,
+                           **self._processor_kw(B))
+        torch.cuda.current_stream(rows.device).synchronize()
+        st = res["status"].cpu().numpy() & 0xFF
+        tok = res["token_ids"].cpu().numpy()
+        lp = res["log_probs"].cpu().numpy()
+        lg = res["logits"].cpu().numpy()
+        out = []
+        for j in range(B):
+            if st[j] != ROW_OK:
+                self.rng = states[j]
+                raise SamplingError({ROW_EMPTY: "cannot sample from empty logits",
+                                     ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
+                                     ROW_PARAM: "invalid sampling parameter",
+                                     ROW_HISTORY: "history too long"}.get(int(st[j]), f"status {int(st[j])}"))
+            out.append(SampleOutput(int(tok[j]) & 0xFFFFFFFF, float(lp[j]), float(lg[j])))
+        return out

@@ -39,6 +39,13 @@ def test_version_string():
     assert b"gfx950" in S.lib().lmrs_sampling_version()
 
 
+def test_no_workspace_is_needed():
+    # every working set is in LDS and registers (no device call is made)
+    L = S.lib()
+    for B, V, dt, H in ((256, 128256, S.DTYPE_BF16, 2048), (512, 256000, S.DTYPE_F32, 512), (1, 1, 0, 0)):
+        assert L.lmrs_sample_workspace_size(B, V, dt, H) == 0
+
+
 def test_args_struct_layout_matches_header(tmp_path):
     # compile the header with the C compiler and compare every field offset
     fields = [f for f, _ in S.SampleArgs._fields_]

@@ -126,3 +126,88 @@ def test_generate_loop_counts_up():
     got = E.generate(model, [[1, 2], [9], [12]], [E.GenerationConfig(4), E.GenerationConfig(3), E.GenerationConfig(6)],
                      eos_token=14)
     assert got == [[3, 4, 5, 6], [10, 11, 12], [13]]
+
+
+# ---------------------------------------------------------------------------
+# the wire format, the sequence state machine and the worker's batch
+# ---------------------------------------------------------------------------
+
+def test_generate_params_wire_format():
+    # defaults (openai.rs:153-157) and the f32 -> f64 widening of
+    # ServerEngine::generate (server/engine.rs:115-122)
+    d = E.GenerateParams()
+    assert (d.max_tokens, d.temperature, d.top_p, d.top_k, d.stop) == (128, 1.0, 1.0, None, ())
+    g = E.GenerateParams(temperature=0.7, top_p=0.9, top_k=40).to_generation_config()
+    assert g.temperature == float(np.float32(0.7)) == 0.699999988079071
+    assert g.top_p == float(np.float32(0.9)) and g.top_k == 40
+    # the widened value is the one the sampler's Temperature holds
+    assert E.sampler_for(g).temperature == 0.699999988079071
+    r = E.GenerateParams.from_request({"max_tokens": None, "temperature": 0.5, "stop": ["\n"]})
+    assert (r.max_tokens, r.temperature, r.top_p, r.top_k, r.stop) == (128, 0.5, 1.0, None, ("\n",))
+    with pytest.raises(ValueError):
+        E.GenerateParams(temperature=0.0).to_generation_config()
+
+
+def test_sequence_state_machine():
+    O = S.SampleOutput
+    # the doctest of sequence.rs:36-47
+    seq = E.Sequence(7, [10, 11], 2, 99)
+    assert seq.status is E.SequenceStatus.WAITING
+    seq.mark_processed(2)
+    seq.append_sample(O(12, 0.0, 4.0))
+    assert seq.pending_tokens() == [12] and seq.status is E.SequenceStatus.RUNNING
+    # EOS is kept and finishes with Eos (sequence.rs:160-172)
+    seq.append_sample(O(99, -0.5, 3.0))
+    assert seq.generated_token_ids() == [12, 99]
+    assert seq.status is E.SequenceStatus.FINISHED and seq.finish_reason is E.FinishReason.EOS
+    with pytest.raises(E.SequenceError):
+        seq.append_sample(O(1, 0.0, 0.0))
+    # Length at max_new_tokens
+    s2 = E.Sequence(1, [5], 2)
+    s2.append_sample(O(6, 0.0, 0.0))
+    s2.append_sample(O(7, 0.0, 0.0))
+    assert s2.finish_reason is E.FinishReason.LENGTH and str(s2.finish_reason) == "length"
+    with pytest.raises(E.SequenceError):
+        E.Sequence(2, [], 4)
+    s3 = E.Sequence(3, [1, 2], 4)
+    with pytest.raises(E.SequenceError):
+        s3.mark_processed(3)
+    # status.rs:91-99
+    E.validate_transition(E.SequenceStatus.WAITING, E.SequenceStatus.RUNNING)
+    with pytest.raises(E.SequenceError):
+        E.validate_transition(E.SequenceStatus.FINISHED, E.SequenceStatus.RUNNING)
+
+
+@pytest.mark.gpu
+def test_run_batch_matches_successive_sample_calls():
+    """run_batch (one launch) against the reference worker's entry loop: B
+    successive Sampler::sample calls on one sampler give the same outputs
+    and leave its LCG in the same state, also when an entry fails."""
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    rng = np.random.default_rng(5)
+    B, V = 12, 4096
+    x = torch.from_numpy(rng.normal(0, 2.0, (B, 1, V)).astype(np.float32)).to(torch.bfloat16).cuda()
+
+    def sampler():
+        s = S.Sampler(S.SamplerConfig(S.TopK(20)).with_seed(42))
+        s.push_processor(S.Temperature(0.8))
+        return s
+
+    a, b = sampler(), sampler()
+    got = E.run_batch(a, x, list(range(100, 100 + B)))
+    want = [b.sample(x[j, -1]) for j in range(B)]
+    assert [o.sequence_id for o in got] == list(range(100, 100 + B))
+    assert [o.sample for o in got] == want and a.rng == b.rng
+    # an entry that fails (a NaN row) stops the batch where the loop stops
+    y = x.clone()
+    y[5, 0, 7] = float("nan")
+    a, b = sampler(), sampler()
+    with pytest.raises(S.SamplingError):
+        E.run_batch(a, y, list(range(B)))
+    with pytest.raises(S.SamplingError):
+        for j in range(B):
+            b.sample(y[j, -1])
+    assert a.rng == b.rng
