@@ -783,6 +783,363 @@ __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 
   return idx;
 }
 
+// Elements of a chunk (four packed key words) with a key in [lo, hi].
+__device__ __forceinline__ uint32_t chunk_matches_keys(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                                       uint32_t lo, uint32_t hi) {
+  const uint32_t w[4] = {w0, w1, w2, w3};
+  uint32_t n = 0u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t key = (w[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+    n += (key >= lo && key <= hi) ? 1u : 0u;
+  }
+  return n;
+}
+
+// find_jth_stream on the keys the load pass left in registers: the same
+// ordered search without a second read of the row.
+template <int NCH>
+__device__ __forceinline__ uint32_t find_jth_regs(FastShared &sh, const uint32_t (&k)[NCH][4], int nchunks,
+                                                  uint32_t nmem, uint32_t lo, uint32_t hi, uint32_t j) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t *slot_cnt = sh.u32(kOffSlotCnt), *tcnt = sh.u32(kOffTcnt);
+  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  for (int i = tid; i < NCH * kFW; i += kFT) slot_cnt[i] = 0u;
+  if (tid == 0) sh.bsel[4] = 0u;
+  __syncthreads();
+  const int ft = fresh_tid();
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    const uint32_t n = (s * kFT + ft < nchunks) ? chunk_matches_keys(k[s][0], k[s][1], k[s][2], k[s][3], lo, hi) : 0u;
+    if (__ballot(n != 0u)) {
+      const uint32_t t = wave_sum(n);
+      if (lane == 0) atomicAdd(&slot_cnt[s * kFW + wave], t);
+    }
+  });
+  for (uint32_t m = tid; m < nmem; m += kFT) {
+    const int dl = member_delta(mkey[m], lo, hi);
+    const uint32_t ch = midx[m] >> 3;
+    if (dl) atomicAdd(&slot_cnt[(ch / kFT) * kFW + ((ch % kFT) >> 6)], (uint32_t)dl);
+  }
+  __syncthreads();
+  if (tid < NCH) {  // per-slot totals
+    uint32_t tot = 0;
+    for (int w = 0; w < kFW; ++w) tot += slot_cnt[tid * kFW + w];
+    tcnt[tid] = tot;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t acc = 0, sstar = NCH - 1, before = 0;
+    for (int s = 0; s < NCH; ++s) {
+      const uint32_t tot = tcnt[s];
+      if (acc + tot >= j) {
+        sstar = (uint32_t)s;
+        before = acc;
+        break;
+      }
+      acc += tot;
+    }
+    sh.bsel[0] = sstar;
+    sh.bsel[1] = before;
+  }
+  __syncthreads();
+  const int sstar = (int)uniform(sh.bsel[0]);
+  const uint32_t jr = j - uniform(sh.bsel[1]);
+  tcnt[tid] = 0u;
+  if (tid < 8) sh.chunk_z[tid] = 0xFFFFFFFFu;
+  __syncthreads();
+  for (uint32_t m = tid; m < nmem; m += kFT) {  // members of slot sstar, per owner row thread
+    const int dl = member_delta(mkey[m], lo, hi);
+    const uint32_t ch = midx[m] >> 3;
+    if (dl && (int)(ch / kFT) == sstar) atomicAdd(&tcnt[ch % kFT], (uint32_t)dl);
+  }
+  __syncthreads();
+  // this thread's chunk of slot sstar, selected from the registers
+  uint32_t w0 = 0u, w1 = 0u, w2 = 0u, w3 = 0u;
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    const bool here = s == sstar;
+    w0 = here ? k[s][0] : w0;
+    w1 = here ? k[s][1] : w1;
+    w2 = here ? k[s][2] : w2;
+    w3 = here ? k[s][3] : w3;
+  });
+  const int chs = sstar * kFT + tid;
+  uint32_t mine = tcnt[tid];
+  if (chs < nchunks) mine += chunk_matches_keys(w0, w1, w2, w3, lo, hi);
+  uint32_t tot;
+  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);
+  if (excl < jr && jr <= excl + mine) {
+    sh.bsel[2] = (uint32_t)chs;  // the chunk
+    sh.bsel[3] = jr - excl;      // rank inside it
+  }
+  __syncthreads();
+  const uint32_t cstar = uniform(sh.bsel[2]), need0 = uniform(sh.bsel[3]);
+  for (uint32_t m = tid; m < nmem; m += kFT)
+    if ((midx[m] >> 3) == cstar) sh.chunk_z[midx[m] & 7u] = mkey[m] >> 16;
+  __syncthreads();
+  if ((uint32_t)chs == cstar) {  // the owner of the chunk picks the element
+    const uint4 w = make_uint4(w0, w1, w2, w3);
+    uint32_t need = need0, pick = cstar * 8u;
+    for (uint32_t e = 0; e < 8u; ++e) {
+      const uint32_t zm = sh.chunk_z[e];
+      const uint32_t key = zm != 0xFFFFFFFFu ? zm : chunk_key(w, e);
+      if (key >= lo && key <= hi) {
+        if (need == 1u) {
+          pick = cstar * 8u + e;
+          break;
+        }
+        need -= 1u;
+      }
+    }
+    sh.bsel[4] = pick;
+  }
+  __syncthreads();
+  const uint32_t idx = uniform(sh.bsel[4]);
+  __syncthreads();
+  return idx;
+}
+
+// ---- the full distribution from the window of top keys ----------------------------
+//
+// A row's mass sits in its top keys: the window pass counts, by LDS atomics
+// into one bin per thread, only the elements whose z key lies within kWin
+// keys of the largest, and adds every other element's weight exp(y - Mb) in
+// f32 (per chunk; f64 across chunks).  That sum enters only the total mass,
+// where an error of 3e-7 relative moves the draw's target by that fraction:
+// inside the 1e-6 margin that flags a row as near a boundary.  Keys whose y
+// lies more than kSkip below a lower bound of the row's maximum are neither
+// counted nor summed: at most V e^-kSkip (< 2e-11) of the largest weight, 1,
+// which a draw reaches only through the rounding fallback, and then the row
+// takes the 65536-bin path.  The cuts and
+// the draw then work on the window's entries as the 65536-bin path does on
+// all of them.  A row whose top-k, min-p or nucleus cut, or whose target, lies
+// below the window's last complete tie group goes to the 65536-bin path.
+constexpr int kWin = kFT;                      // window keys: one bin per thread
+constexpr float kSkip = 37.0f;                 // e^-37 < 1e-16
+constexpr int kOffWinHist = 4096;              // views inside the SelState region, free here
+constexpr int kOffWinKey = kOffWinHist + kWin * 4;
+constexpr int kOffWinCnt = kOffWinKey + kWin * 4;
+constexpr int kOffWinMass = kOffWinCnt + kWin * 4;
+static_assert(kOffTcnt + kFT * 4 <= kOffWinHist && kOffWinMass + kWin * 8 <= kOffWhist, "window views");
+
+// Returns false (uniformly, with the registers and the member list intact)
+// when the row needs the 65536-bin path.
+template <int NCH>
+__device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_args &a, int r, const RowCfg &c,
+                                            const uint32_t (&k)[NCH][4], int nchunks, uint32_t nmem, bool hist,
+                                            uint32_t mx, uint32_t zmem, uint32_t zlow_max, bool k_on) {
+  const int tid = threadIdx.x;
+  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  // no element's z key exceeds this: the raw chunk maxima (members' raw keys
+  // included) and the members' z keys
+  const uint32_t zhb = block_max<kFW>(max(mx, zmem), sh.uscr);
+  if (zhb <= kNegInfKey16 || zhb >= 0xFF80u) return false;  // all -inf, or +inf: the 65536-bin path decides
+  uint32_t zlo = zhb >= kNegInfKey16 + (uint32_t)kWin ? zhb - (uint32_t)(kWin - 1) : kNegInfKey16 + 1u;
+  const float Mb = key16_value(temp_key16(zhb, c));  // at least every element's y
+  // zlow_max is an element's z key: its y is at most the row's maximum; the
+  // chunks whose largest z key lies below zskip hold only weights below e^-kSkip
+  const float ys = key16_value(temp_key16(zlow_max, c)) - kSkip;
+  uint32_t zskip = zlow_max;  // the lowest key whose y reaches ys (zlow_max's does)
+  for (uint32_t lo = kNegInfKey16; lo < zskip;) {
+    const uint32_t mid = lo + ((zskip - lo) >> 1);
+    if (key16_value(temp_key16(mid, c)) >= ys)
+      zskip = mid;
+    else
+      lo = mid + 1u;
+  }
+  zlo = max(zlo, zskip);  // keys below zskip are neither counted nor summed
+  // every element below the window weighs less than e^-kSkip: a cut that
+  // falls there changes the kept mass by under 2e-11 of it, and the draw's
+  // target can reach those elements only through the rounding fallback
+  const bool tail_negligible = zlo == zskip;
+  // weight exp(y - Mb) as exp2(y log2(e) - Mb log2(e)), one multiply-add
+  const float l2e = 1.4426950408889634f, mb2 = Mb * l2e;
+  uint32_t *wh = sh.u32(kOffWinHist);
+  wh[tid] = 0u;
+  __syncthreads();
+  double below = 0.0;
+  const int ft = fresh_tid();
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    const int ch = s * kFT + ft;
+    if (ch < nchunks && chunk_max(k[s]) >= zskip) {
+      const uint32_t m8 = hist ? chunk_m8(sh, (uint32_t)ch) : 0u;  // members enter by their z key
+      float acc = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t key = (k[s][e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+        const bool mem = (m8 >> e) & 1u;
+        if (!mem && key >= zlo) atomicAdd(&wh[zhb - key], 1u);
+        const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(key, c)), l2e, -mb2));
+        acc += (mem || key >= zlo || key < zskip) ? 0.0f : w;
+      }
+      below += (double)acc;
+    }
+  });
+  for (uint32_t m = tid; m < nmem; m += kFT) {
+    const uint32_t zk = mkey[m] >> 16;
+    if (zk >= zlo)
+      atomicAdd(&wh[zhb - zk], 1u);
+    else if (zk >= zskip)
+      below += (double)__builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(zk, c)), l2e, -mb2));
+  }
+  below = block_sum<kFW>(below, sh.dscr);  // (its barriers order the histogram too)
+  // entries: thread t holds bin t, key zhb - t, in descending key order
+  const uint32_t cn = wh[tid];
+  uint32_t nbu;
+  const uint32_t pos = block_exclusive_scan<kFW>(cn != 0u ? 1u : 0u, sh.uscr, &nbu);
+  uint32_t *ekey = sh.u32(kOffWinKey), *ecnt = sh.u32(kOffWinCnt);
+  if (cn) {
+    ekey[pos] = zhb - (uint32_t)tid;
+    ecnt[pos] = cn;
+  }
+  __syncthreads();
+  const int nb = (int)nbu;
+  if (nb == 0) return false;
+  auto ykey_of = [&](int e) { return temp_key16(ekey[e], c); };
+  const float M = key16_value(ykey_of(0));
+  if (!((double)Mb - (double)M <= 40.0)) return false;  // the f32 weights below would lose their range
+  auto weight_of = [&](int e) { return exp((double)(key16_value(ykey_of(e)) - M)); };
+  // inclusive count and mass prefixes, entry e at thread e
+  uint32_t *cincl = ecnt;  // (in place: each thread reads its count first)
+  double *mincl = (double *)sh.u32(kOffWinMass);
+  const uint32_t ce = tid < nb ? ecnt[tid] : 0u;
+  const double me = tid < nb ? (double)ce * weight_of(tid) : 0.0;
+  uint32_t ctot;
+  double mtot;
+  const uint32_t cex = block_exclusive_scan<kFW>(ce, sh.uscr, &ctot);
+  const double mex = block_exclusive_scan<kFW>(me, sh.dscr, &mtot);
+  if (tid < nb) {
+    cincl[tid] = cex + ce;
+    mincl[tid] = mex + me;
+  }
+  __syncthreads();
+  auto group_head = [&](int e) {
+    const uint32_t y = ykey_of(e);
+    while (e > 0 && ykey_of(e - 1) == y) --e;
+    return e;
+  };
+  auto group_tail = [&](int e) {
+    const uint32_t y = ykey_of(e);
+    while (e + 1 < nb && ykey_of(e + 1) == y) ++e;
+    return e;
+  };
+  auto cnt_of = [&](int e) { return cincl[e] - (e > 0 ? cincl[e - 1] : 0u); };
+  auto cnt_excl = [&](int e) { return e > 0 ? cincl[e - 1] : 0u; };
+  auto mass_excl = [&](int e) { return e > 0 ? mincl[e - 1] : 0.0; };
+  // the last tie group continues below the window when key zlo - 1 has its
+  // y: entries [0, hg) are complete
+  const int hg = temp_key16(zlo - 1u, c) == ykey_of(nb - 1) ? group_head(nb - 1) : nb;
+  if (hg == 0) return false;
+  auto first_mass = [&](double target, int last) {  // first entry <= last reaching target; -1 if none
+    int f = 0x7FFFFFFF;
+    if (tid <= last && mincl[tid] >= target) f = tid;
+    f = block_min<kFW>(f, sh.iscr);
+    return f == 0x7FFFFFFF ? -1 : f;
+  };
+  const double total = mtot + below * exp((double)Mb - (double)M);
+  // candidates.  last_h: head of the last kept tie group, or nb when the
+  // kept set runs below the window (then no window group is cut short)
+  int last_e = hg - 1, last_h = nb;
+  uint32_t last_keep = 0u;
+  double cand_mass = total;
+  if (k_on) {
+    int f = 0x7FFFFFFF;
+    if (tid < hg && cincl[tid] >= (uint32_t)c.top_k) f = tid;
+    f = block_min<kFW>(f, sh.iscr);
+    if (f != 0x7FFFFFFF) {
+      last_h = group_head(f);
+      last_e = group_tail(f);
+      last_keep = (uint32_t)c.top_k - cnt_excl(last_h);
+      cand_mass = mass_excl(last_h) + (double)last_keep * weight_of(last_h);
+    } else if (!tail_negligible) {
+      return false;  // the k-th token lies below the window
+    }
+  }
+  int32_t flags = 0;
+  if (c.min_p >= 0.0) {  // the min-p cut (min_p.rs:45-53)
+    const double thr = minp_threshold(M, c);
+    if (!(thr == thr)) {  // NaN threshold: softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    const uint32_t ymp = minp_low_key(kNegInfKey16, ykey_of(0), thr, [](uint32_t kk) { return key16_value(kk); });
+    int fm = 0x7FFFFFFF;
+    if (tid < nb && ykey_of(tid) < ymp) fm = tid;
+    fm = block_min<kFW>(fm, sh.iscr);
+    if (fm == 0x7FFFFFFF) fm = nb;
+    if (fm == 0) {  // not reached: the maximum always passes a non-NaN threshold
+      if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    if (fm - 1 < last_h) {  // the cut ends above the top-k set's last tie group
+      // ... known when a window entry fails the cut and every kept entry is
+      // complete, or when the cut falls among the negligible elements
+      if (fm < nb) {
+        if (fm > hg) return false;
+        last_e = fm - 1;
+        last_h = group_head(last_e);
+        last_keep = cnt_excl(last_e) + cnt_of(last_e) - cnt_excl(last_h);
+        cand_mass = mincl[last_e];
+      } else if (!tail_negligible) {
+        return false;
+      }
+    }
+    if (minp_near(key16_value(ymp), M, thr) || (ymp > kNegInfKey16 && minp_near(key16_value(ymp - 1u), M, thr)))
+      flags |= LMRS_ROW_NEAR_BOUNDARY;
+  }
+  if (!(__builtin_isfinite(cand_mass) && cand_mass > 0.0)) {  // (strategies/mod.rs:39-43)
+    if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
+    return true;
+  }
+  double kept_mass = cand_mass;
+  if (c.top_p < 1.0) {  // nucleus cut (top_p.rs:45-58) over the candidates
+    const double tp = c.top_p * cand_mass;
+    const int f = first_mass(tp, last_e);
+    if (f < 0) return false;  // the nucleus runs below the window
+    const int h = group_head(f), t = group_tail(f);
+    const double wg = weight_of(h), mx2 = mass_excl(h);
+    const uint32_t gmax = (h == last_h) ? last_keep : cincl[t] - cnt_excl(h);
+    double jj = ceil((tp - mx2) / wg);
+    if (!(jj >= 1.0)) jj = 1.0;
+    if (jj > (double)gmax) jj = (double)gmax;
+    const uint32_t jp = (uint32_t)jj;
+    kept_mass = mx2 + (double)jp * wg;
+    const double acc = kept_mass / cand_mass, prev = (kept_mass - wg) / cand_mass;
+    double m = c.top_p - prev;
+    if (acc - c.top_p < m) m = acc - c.top_p;
+    if (m < 1e-6) flags |= LMRS_ROW_NEAR_BOUNDARY;
+    last_h = h;
+    last_e = t;
+    last_keep = jp;
+  }
+  // the draw (softmax_choice, strategies/mod.rs:44-54)
+  const double target = c.u * kept_mass;
+  const int f = first_mass(target, last_e);
+  if (f < 0) return false;  // below the window (or the rounding fallback: the 65536-bin path has it)
+  const int h = group_head(f), tl = group_tail(f);
+  const double mx2 = mass_excl(h), wg = weight_of(h);
+  const uint32_t gmax = (h == last_h) ? last_keep : cincl[tl] - cnt_excl(h);
+  double jj = ceil((target - mx2) / wg);
+  if (!(jj >= 1.0)) jj = 1.0;
+  if (jj > (double)gmax) jj = (double)gmax;
+  const uint32_t jt = (uint32_t)jj;
+  const uint32_t zhi = uniform(ekey[h]), zlo2 = uniform(ekey[tl]);
+  const float yv = key16_value(ykey_of(h));
+  const bool first_tok = (h == 0 && jt == 1u), last_tok = (h == last_h && jt == gmax);
+  __syncthreads();  // the window views are dead
+  const uint32_t token = find_jth_regs<NCH>(sh, k, nchunks, nmem, zlo2, zhi, jt);
+  if (tid == 0) {
+    const double lo_c = (mx2 + (double)(jt - 1u) * wg) / kept_mass, hi_c = lo_c + wg / kept_mass;
+    double m = 1.0;
+    if (!first_tok && fabs(c.u - lo_c) < m) m = fabs(c.u - lo_c);
+    if (!last_tok && fabs(hi_c - c.u) < m) m = fabs(hi_c - c.u);
+    write_row(a, r, token, (float)log(wg / kept_mass), yv, flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+  }
+  return true;
+}
+
 // ---- one row ----------------------------------------------------------------------
 
 // Returns false (uniformly) when the row must go to the generic engine,
@@ -1012,6 +1369,10 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     finish_sorted<TR, kFT>(ss, c, a, r, K);
     return true;
   }
+
+  // ---- the window of top keys: the full distribution, and top-k cuts whose
+  // k-th token lies in it -------------------------------------------------------
+  if (full_window<NCH>(sh, a, r, c, k, nchunks, nmem, hist, mx, zmem, tvhi, k_on)) return true;
 
   if (k_on && c.top_k <= kGatherCap) {  // ---- mid k -------------------------------
     const uint32_t K = (uint32_t)c.top_k;

@@ -447,3 +447,54 @@ def test_min_p_on_every_path():
         assert_parity(rep, f"min-p-{dtype}-{V}")
         st = list(r["status"][-len(specials):])
         assert st == [0, 1, 0, 0, 0, 2, 1, 2, 2, 1], st
+
+
+def test_window_path_cuts_and_fallbacks():
+    """The bf16 kernel's top-key window (full distribution and top-k > 64):
+    rows it resolves -- top-k and min-p cuts inside it or among the negligible
+    elements below it, an isolated maximum, history members inside and below
+    it -- and rows it hands to the 65536-bin path: the target, the nucleus
+    or the min-p cut below a window whose tail still carries mass."""
+    W = _wl()
+    rng = np.random.default_rng(123)
+    for V in (32000, 128256, 151936):
+        rows, ks, ps, mps, ts, us, hists = [], [], [], [], [], [], []
+
+        def add(x, k=0, p=1.0, mp=-1.0, t=1.0, u=None, h=()):
+            rows.append(x.astype(np.float32))
+            ks.append(k)
+            ps.append(p)
+            mps.append(mp)
+            ts.append(t)
+            us.append(rng.random() if u is None else u)
+            hists.append(list(h))
+
+        heavy = lambda: rng.standard_t(3, V) * 2.5  # noqa: E731
+        normal = lambda s=3.0: rng.normal(0.0, s, V)  # noqa: E731
+        add(heavy(), k=1000, t=0.5)                  # k-th token among the negligible elements
+        add(heavy(), k=300, p=0.9, t=1.3)            # k-th token inside the window
+        add(normal(), k=3000)                        # k-th token inside the window (N(0, 3))
+        x = normal(1.0)
+        x[rng.integers(V)] = 500.0
+        add(x)                                       # an isolated maximum: a one-entry window
+        add(normal(), u=0.99995)                     # target below the window: 65536-bin path
+        add(normal(1.0), p=0.9999, t=2.0)            # nucleus below the window: 65536-bin path
+        add(normal(), mp=1e-9)                       # min-p cut below a window with mass under it
+        add(heavy(), mp=1e-30, t=0.5)                # min-p cut among the negligible elements
+        add(normal(), p=0.9, mp=0.01, t=0.8)         # min-p and nucleus inside the window
+        x = np.full(V, -np.inf)
+        x[rng.choice(V, 40, replace=False)] = rng.normal(0, 1, 40)
+        add(x, k=200)                                # -inf everywhere but 40 tokens
+        top = None
+        for t in (1.0, 0.7):                         # members inside and below the window
+            x = normal()
+            top = np.argsort(-x)[:400]
+            add(x, p=0.95, t=t, h=list(top[::2]) + list(rng.integers(0, V, 300)))
+        B = len(rows)
+        xx = W.f32_to_bf16_bits(np.stack(rows))
+        w = _mk(xx, k=np.array(ks, np.int32), p=np.array(ps), mp=np.array(mps), t=np.array(ts), u=np.array(us),
+                rep=[1.3] * B, pres=[0.4] * B, freq=[0.2] * B, history=hists)
+        print(f"[case] window path V={V} B={B}", flush=True)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"window-{V}", rep)
+        assert_parity(rep, f"window-{V}")
