@@ -52,6 +52,14 @@ def workload_config(w) -> dict:
             "history_per_row": w.hist_len}
 
 
+def kernel_label(w) -> str:
+    """The kernel lmrs_sample_fwd launches for this workload (its dispatch rule)."""
+    if w.dtype == "bf16" and w.vocab % 8 == 0 and 0 < w.vocab <= 40 * 4096:
+        nch = next(n for n in (8, 16, 32, 40) if w.vocab <= n * 4096)
+        return f"bf16_fast_kernel<{nch}> (one launch per step)"
+    return f"generic_sample_kernel<{0 if w.dtype == 'bf16' else 2}> (one launch per step)"
+
+
 def read_traffic(name: str):
     """HBM bytes per launch from the committed counter summary (None if absent)."""
     if name != "C3" or not os.path.exists(TRAFFIC_FILE):
@@ -212,7 +220,7 @@ def main() -> int:
         "config": workload_config(w),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "algorithmic_bytes": alg, "kernel": "bf16_fast_kernel<32> (one launch per step)"},
+                     "algorithmic_bytes": alg, "kernel": kernel_label(w)},
         "rotating_buffers": nrot,
     }
     if not args.no_cpu:
