@@ -1689,7 +1689,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
 template <int NCH>
 __global__ void __launch_bounds__(kFT) bf16_fast_kernel(lmrs_sample_args a) {
   __shared__ FastOrGeneric sh;
-  const int r = blockIdx.x;
+  const int r = xcd_spread_row((int)blockIdx.x, (int)gridDim.x);
   if (fast_row<NCH>(sh.f, a, r)) return;
   __syncthreads();
   generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, a, r, 1);

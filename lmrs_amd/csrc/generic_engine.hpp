@@ -637,7 +637,7 @@ __device__ __forceinline__ void generic_row(GenericShared &sh, const lmrs_sample
 template <int DT>
 __global__ void __launch_bounds__(kThreads) generic_sample_kernel(lmrs_sample_args a, int vec) {
   __shared__ GenericShared sh;
-  generic_row<DT>(sh, a, blockIdx.x, vec);
+  generic_row<DT>(sh, a, xcd_spread_row((int)blockIdx.x, (int)gridDim.x), vec);
 }
 
 // LogitsProcessor::process for the three reference processors, batched.
