@@ -348,13 +348,15 @@ __device__ __forceinline__ uint32_t wave_reserve(uint32_t n, uint32_t *counter) 
 // ---- history members ------------------------------------------------------------
 
 // This thread's history ids (strided by the block), issued as explicit loads;
-// positions past the end re-read the first id and are ignored later.
+// positions past the end re-read the first id and are ignored later.  Rows
+// without a history load `dummy` instead, so that every row issues the same
+// number of loads (the waits count them).
 __device__ __forceinline__ void issue_history_ids(uint32_t (&hid)[kHistPer], const lmrs_sample_args &a,
-                                                  const RowCfg &c) {
+                                                  const RowCfg &c, bool hist, const void *dummy) {
 #pragma unroll
   for (int q = 0; q < kHistPer; ++q) {
     const int64_t j = (int64_t)threadIdx.x + (int64_t)q * kFT;
-    hid[q] = issue_load_b32(a.hist_ids + c.h_begin + (j < c.h_len ? j : 0));
+    hid[q] = issue_load_b32(hist ? a.hist_ids + c.h_begin + (j < c.h_len ? j : 0) : (const uint32_t *)dummy);
   }
 }
 
@@ -1157,30 +1159,37 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   u32x4 kv[NCH];
   uint32_t k[NCH][4];
 
-  // Parameters through scalar loads (no store precedes them), then the
-  // history ids (requests queue in issue order across the whole chip: ids
-  // requested after the logits would arrive after them) and the row's first
-  // kEarly slots.  The load pass requests slot s + kEarly when it processes
-  // slot s, so that a wave never waits long on a full memory queue with
-  // data at hand.  The member tables are built inside the load pass, after
-  // slot kHistAt, while the row streams in; the members' raw logits are
-  // requested right after them and their keys computed kAhead + 1 slots
-  // later.  No path leaves before the load pass consumes the row.
-  const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
-  const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
+  // The row's first kPre slots (their addresses need only the kernel
+  // arguments), then the parameters through scalar loads (no store precedes
+  // them), the history ids (always kHistPer loads) and the rest of the first
+  // kEarly slots.  Requests queue in issue order across the chip: two slots
+  // ahead of the parameters hide part of their latency (measured: 0.15 us on
+  // C3), eight delay them and the history by more than they gain.  The load
+  // pass requests slot s + kEarly when it processes slot s, so that a wave
+  // never waits long on a full memory queue with data at hand.  The member
+  // tables are built inside the load pass, after slot kHistAt, while the row
+  // streams in; the members' raw logits are requested right after them and
+  // their keys computed kAhead + 1 slots later.  No path leaves before the
+  // load pass consumes the row.
   constexpr int kEarly = NCH / 4;     // slots in flight ahead of the one being processed
   constexpr int kHistAt = 2;          // the slot after which the member tables are built
   constexpr int kAhead = kEarly;      // (a deeper queue from slot kHistAt on measured slower)
   constexpr int kKeysAt = kHistAt + kAhead + 1;  // the slot whose wait covers the members' loads
-  static_assert(kKeysAt < NCH && kAhead >= kEarly, "member keys inside the load pass");
+  constexpr int kPre = 2;             // slots requested before the parameters
+  static_assert(kKeysAt < NCH && kAhead >= kEarly && kPre <= kHistAt && kPre <= kEarly,
+                "member keys inside the load pass");
   auto issue_slot = [&](int s) {
     const int ch = s * kFT + tid;
     return issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
   };
-  uint32_t hid[kHistPer];
-  if (hist) issue_history_ids(hid, a, c);
 #pragma unroll
-  for (int s = 0; s < kEarly; ++s) kv[s] = issue_slot(s);
+  for (int s = 0; s < kPre; ++s) kv[s] = issue_slot(s);
+  const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
+  const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
+  uint32_t hid[kHistPer];
+  issue_history_ids(hid, a, c, hist, rowp);
+#pragma unroll
+  for (int s = kPre; s < kEarly; ++s) kv[s] = issue_slot(s);
   clear_tables(sh, hist, nwords);
 
   // The load pass: keys, chunk maxima (to LDS as their words fill), the NaN
@@ -1203,9 +1212,11 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     } else {
       if constexpr (s + kAhead < NCH) kv[s + kAhead] = issue_slot(s + kAhead);
     }
-    // loads issued after slot s's: later slots, and the members' for the
-    // slots requested before them and waited for after them
-    constexpr int younger = last - s + (s > kHistAt && s <= kHistAt + kAhead ? kMemPer : 0);
+    // loads issued after slot s's: later slots; the history ids for the
+    // first kPre slots; the members' for the slots requested before them and
+    // waited for after them
+    constexpr int younger = last - s + (s > kHistAt && s <= kHistAt + kAhead ? kMemPer : 0) +
+                            (s < kPre ? kHistPer : 0);
     wait_loads<younger>(kv[s]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1229,10 +1240,12 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     cmw = (s & 1) ? (cmw | (cmx << 16)) : cmx;
     if constexpr ((s & 1) == 1 || s == NCH - 1) cml[(s >> 1) * kFT] = cmw;
     if constexpr (s == kHistAt) {
-      // the history ids are older than this slot's loads: complete
-      if (hist) {
+      // the history ids, followed by slots kPre .. last; waited for on every
+      // path (see the member loads below)
+      constexpr int hyounger = last - kPre + 1;
 #pragma unroll
-        for (int q = 0; q < kHistPer; ++q) wait_loads<younger>(hid[q]);
+      for (int q = 0; q < kHistPer; ++q) wait_loads<hyounger>(hid[q]);
+      if (hist) {
         mark_history(sh, hid, c.h_len, V);
         nmem = rank_members(sh, nwords);
         if (nmem <= (uint32_t)kFastMembers) count_members(sh, hid, c.h_len, V);
