@@ -498,3 +498,43 @@ def test_window_path_cuts_and_fallbacks():
         rep = compare(run_gpu(w), run_oracle(w))
         _report(f"window-{V}", rep)
         assert_parity(rep, f"window-{V}")
+
+
+def test_randomized_rows_every_path():
+    """Seeded random rows over the distributions and parameters the paths
+    branch on (normal, heavy-tailed, flat, spiked, ties; temperature; top-k
+    from 1 to beyond the window; top-p; min-p; histories), against the oracle."""
+    W = _wl()
+    rng = np.random.default_rng(2024)
+    for V, B in ((32000, 160), (128256, 96)):
+        rows, ks, ps, mps, ts, hists = [], [], [], [], [], []
+        for _ in range(B):
+            kind = rng.integers(6)
+            if kind == 0:
+                x = rng.normal(0, rng.uniform(0.3, 4.0), V)
+            elif kind == 1:
+                x = rng.standard_t(rng.uniform(1.5, 5.0), V) * rng.uniform(0.5, 3.0)
+            elif kind == 2:
+                x = rng.uniform(-1, 1, V) * 0.01          # nearly flat
+            elif kind == 3:
+                x = rng.normal(0, 1, V)
+                x[rng.choice(V, rng.integers(1, 20), replace=False)] += rng.uniform(5, 30)
+            elif kind == 4:
+                x = rng.integers(-8, 8, V).astype(np.float64) / 2  # wide ties
+            else:
+                x = rng.gumbel(0, 2.0, V)
+            rows.append(x.astype(np.float32))
+            ks.append(int(rng.choice([0, 0, 1, 2, 10, 50, 64, 65, 300, 1000, 4096, 5000, V + 3])))
+            ps.append(float(rng.choice([1.0, 1.0, rng.uniform(0.05, 1.0), 0.999])))
+            mps.append(float(rng.choice([-1.0, -1.0, -1.0, 0.0, rng.uniform(0, 0.5), 10 ** rng.uniform(-12, -1)])))
+            ts.append(float(rng.choice([1.0, 1.0, rng.uniform(0.3, 2.5)])))
+            hists.append(list(rng.integers(0, V, int(rng.choice([0, 0, 50, 600])))))
+        B = len(rows)
+        xx = W.f32_to_bf16_bits(np.stack(rows))
+        w = _mk(xx, k=np.array(ks, np.int32), p=np.array(ps), mp=np.array(mps), t=np.array(ts),
+                rep=rng.uniform(0.8, 1.5, B).astype(np.float32), pres=rng.uniform(-0.5, 1.0, B).astype(np.float32),
+                freq=rng.uniform(0, 0.5, B).astype(np.float32), u=rng.random(B), history=hists)
+        print(f"[case] randomized V={V} B={B}", flush=True)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"randomized-{V}", rep)
+        assert_parity(rep, f"randomized-{V}")
