@@ -100,6 +100,51 @@ def cpu_baseline(w, gpu_out, seconds: float):
     return base, parity
 
 
+def stream_ceiling(bufs, steps: int, warmup: int, dev) -> float:
+    """GB/s of a read-only kernel with the sampler's access shape (one
+    512-thread workgroup per row, pipelined non-temporal 16-byte loads:
+    lmrs_amd/csrc/stream_probe.hip) over the same rotating buffers, timed like
+    the step on its own stream.  None when the probe library is not built."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "lmrs_amd", "liblmrs_stream_probe.so")
+    if not os.path.exists(path):
+        return None
+    L = ctypes.CDLL(path)
+    L.lmrs_stream_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32,
+                                    ctypes.c_void_p, ctypes.c_void_p]
+    L.lmrs_stream_probe.restype = ctypes.c_int
+    rows = bufs[0].shape[0]
+    row_bytes = bufs[0].shape[1] * bufs[0].element_size()
+    stride = bufs[0].stride(0) * bufs[0].element_size()
+    if row_bytes % 16 or row_bytes // 16 > 40 * 512:  # beyond the probe's register-resident shapes
+        return None
+    out = torch.empty(rows, dtype=torch.int32, device=dev)
+    s = torch.cuda.Stream(device=dev)
+
+    def launch(i):
+        rc = L.lmrs_stream_probe(ctypes.c_void_p(bufs[i % len(bufs)].data_ptr()), row_bytes, stride, rows,
+                                 ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(s.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"lmrs_stream_probe failed with code {rc}")
+
+    with torch.cuda.stream(s):
+        for i in range(warmup):
+            launch(i)
+        s.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for i in range(steps):
+            launch(i)
+        e1.record(s)
+        e1.synchronize()
+    ms = e0.elapsed_time(e1) / max(1, steps)
+    log(f"bench: streaming read of one buffer (probe) {ms * 1e3:.1f} us")
+    return rows * row_bytes / (ms * 1e-3) / 1e9
+
+
 def copy_calibration(size_mb: int, reps: int) -> None:
     """A plain device copy of known size, for scaling the FETCH_SIZE /
     WRITE_SIZE counters to bytes (run under rocprofv3 --pmc)."""
@@ -191,6 +236,7 @@ def main() -> int:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / max(1, args.steps)
     log(f"bench: {args.steps} steps, {ms * 1e3:.1f} us/step")
+    ceiling = stream_ceiling(bufs, args.steps, args.warmup, dev)
 
     # outputs of the last step (every rotation holds the same logits)
     res = {
@@ -222,6 +268,11 @@ def main() -> int:
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes": alg, "kernel": kernel_label(w)},
         "rotating_buffers": nrot,
+        # secondary denominator: the measured read rate of the same rotating
+        # buffers by a load-only kernel of the sampler's access shape
+        "stream_ceiling": {"achieved": ceiling, "unit": "GB/s",
+                           "kernel": "lmrs_stream_probe (the load pass alone, same access shape)",
+                           "frac": (alg / (ms * 1e-3) / 1e9) / ceiling if ceiling else None},
     }
     if not args.no_cpu:
         log("bench: CPU baseline (oracle) ...")

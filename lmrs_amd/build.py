@@ -35,9 +35,21 @@ FLAGS = [
 ]
 
 
+# bench.py's measured streaming ceiling: a read-only kernel with the sampler's
+# access shape, in a library of its own (not part of the sampling ABI)
+PROBE_LIB = os.path.join(HERE, "liblmrs_stream_probe.so")
+PROBE_SOURCES = ["stream_probe.hip"]
+
+
 def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), *srcs, "-o", LIB + ".tmp"]
+    _build_one(SOURCES, LIB, verbose)
+    _build_one(PROBE_SOURCES, PROBE_LIB, verbose)
+    return LIB
+
+
+def _build_one(sources, lib, verbose):
+    srcs = [os.path.join(CSRC, s) for s in sources]
+    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), *srcs, "-o", lib + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,11 +57,10 @@ def build(verbose: bool = False) -> str:
     errs = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
     if res.returncode != 0:
         sys.stderr.write("\n".join(errs) + "\n")
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {LIB}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {lib}")
     if verbose and errs:
         sys.stderr.write("\n".join(errs) + "\n")
-    os.replace(LIB + ".tmp", LIB)
-    return LIB
+    os.replace(lib + ".tmp", lib)
 
 
 if __name__ == "__main__":

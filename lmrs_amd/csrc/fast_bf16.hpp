@@ -932,7 +932,7 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
                                             const uint32_t (&k)[NCH][4], int nchunks, uint32_t nmem, bool hist,
                                             uint32_t mx, uint32_t zmem, uint32_t zlow_max, bool k_on) {
   const int tid = threadIdx.x;
-  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  const uint32_t *mkey = sh.m_key();
   // no element's z key exceeds this: the raw chunk maxima (members' raw keys
   // included) and the members' z keys
   const uint32_t zhb = block_max<kFW>(max(mx, zmem), sh.uscr);
