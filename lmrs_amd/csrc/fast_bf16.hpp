@@ -675,17 +675,114 @@ __device__ __forceinline__ uint32_t chunk_matches(const uint4 &d, uint32_t lo, u
   return n;
 }
 
-// The j-th (1-based) lowest index among elements whose z key lies in [lo, hi]
-// (members by their z key), on a second read of the row.  Index order is
-// (slot, thread, element): per-slot match counts are reduced into LDS, the
-// slot holding the j-th match is found, and one block scan over that slot's
-// per-thread counts locates the chunk and then the element.
+// Elements of a chunk (four packed key words) with a key in [lo, hi].
+__device__ __forceinline__ uint32_t chunk_matches_keys(const uint4 &w, uint32_t lo, uint32_t hi) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+  uint32_t n = 0u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t key = (x[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+    n += (key >= lo && key <= hi) ? 1u : 0u;
+  }
+  return n;
+}
+
+// The ordered search for the j-th (1-based) lowest index among elements
+// whose z key lies in [lo, hi] (members by their z key).  Index order is
+// (slot, thread, element).  The caller has added each wave's count of
+// matching raw keys per slot to slot_cnt[s * kFW + wave]; this adds the
+// members' net counts, finds the slot holding the j-th match, and, with one
+// block scan over that slot's per-thread counts, the chunk and then the
+// element.  keys_of(s) returns this thread's chunk of slot s as four packed
+// key words (called once, for the chosen slot, by every thread).
+template <int NCH, class KeysOf>
+__device__ __forceinline__ uint32_t locate_jth(FastShared &sh, int nchunks, uint32_t nmem, uint32_t lo,
+                                               uint32_t hi, uint32_t j, KeysOf keys_of) {
+  const int tid = threadIdx.x;
+  uint32_t *slot_cnt = sh.u32(kOffSlotCnt), *tcnt = sh.u32(kOffTcnt);
+  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  for (uint32_t m = tid; m < nmem; m += kFT) {
+    const int dl = member_delta(mkey[m], lo, hi);
+    const uint32_t ch = midx[m] >> 3;
+    if (dl) atomicAdd(&slot_cnt[(ch / kFT) * kFW + ((ch % kFT) >> 6)], (uint32_t)dl);
+  }
+  __syncthreads();
+  if (tid < NCH) {  // per-slot totals
+    uint32_t tot = 0;
+    for (int w = 0; w < kFW; ++w) tot += slot_cnt[tid * kFW + w];
+    tcnt[tid] = tot;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t acc = 0, sstar = NCH - 1, before = 0;
+    for (int s = 0; s < NCH; ++s) {
+      const uint32_t tot = tcnt[s];
+      if (acc + tot >= j) {
+        sstar = (uint32_t)s;
+        before = acc;
+        break;
+      }
+      acc += tot;
+    }
+    sh.bsel[0] = sstar;
+    sh.bsel[1] = before;
+    sh.bsel[4] = 0u;
+  }
+  __syncthreads();
+  const int sstar = (int)uniform(sh.bsel[0]);
+  const uint32_t jr = j - uniform(sh.bsel[1]);
+  tcnt[tid] = 0u;
+  if (tid < 8) sh.chunk_z[tid] = 0xFFFFFFFFu;
+  __syncthreads();
+  for (uint32_t m = tid; m < nmem; m += kFT) {  // members of slot sstar, per owner row thread
+    const int dl = member_delta(mkey[m], lo, hi);
+    const uint32_t ch = midx[m] >> 3;
+    if (dl && (int)(ch / kFT) == sstar) atomicAdd(&tcnt[ch % kFT], (uint32_t)dl);
+  }
+  __syncthreads();
+  const int chs = sstar * kFT + tid;
+  const uint4 w = keys_of(sstar);
+  uint32_t mine = tcnt[tid];
+  if (chs < nchunks) mine += chunk_matches_keys(w, lo, hi);
+  uint32_t tot;
+  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);
+  if (excl < jr && jr <= excl + mine) {
+    sh.bsel[2] = (uint32_t)chs;  // the chunk
+    sh.bsel[3] = jr - excl;      // rank inside it
+  }
+  __syncthreads();
+  const uint32_t cstar = uniform(sh.bsel[2]), need0 = uniform(sh.bsel[3]);
+  for (uint32_t m = tid; m < nmem; m += kFT)
+    if ((midx[m] >> 3) == cstar) sh.chunk_z[midx[m] & 7u] = mkey[m] >> 16;
+  __syncthreads();
+  if ((uint32_t)chs == cstar) {  // the owner of the chunk picks the element
+    uint32_t need = need0, pick = cstar * 8u;
+    for (uint32_t e = 0; e < 8u; ++e) {
+      const uint32_t zm = sh.chunk_z[e];
+      const uint32_t key = zm != 0xFFFFFFFFu ? zm : chunk_key(w, e);
+      if (key >= lo && key <= hi) {
+        if (need == 1u) {
+          pick = cstar * 8u + e;
+          break;
+        }
+        need -= 1u;
+      }
+    }
+    sh.bsel[4] = pick;
+  }
+  __syncthreads();
+  const uint32_t idx = uniform(sh.bsel[4]);
+  __syncthreads();
+  return idx;
+}
+
+// The ordered search on a second read of the row (the 65536-bin path, whose
+// keys have left the registers): per-slot match counts, G slots in flight.
 template <int NCH>
 __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 *src, int nchunks, uint32_t nmem,
                                                     uint32_t lo, uint32_t hi, uint32_t j) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t *slot_cnt = sh.u32(kOffSlotCnt), *tcnt = sh.u32(kOffTcnt);
-  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  uint32_t *slot_cnt = sh.u32(kOffSlotCnt);
   for (int i = tid; i < NCH * kFW; i += kFT) slot_cnt[i] = 0u;
   __syncthreads();
   {
@@ -710,196 +807,44 @@ __device__ __forceinline__ uint32_t find_jth_stream(FastShared &sh, const uint4 
       }
     }
   }
-  for (uint32_t m = tid; m < nmem; m += kFT) {
-    const int dl = member_delta(mkey[m], lo, hi);
-    const uint32_t ch = midx[m] >> 3;
-    if (dl) atomicAdd(&slot_cnt[(ch / kFT) * kFW + ((ch % kFT) >> 6)], (uint32_t)dl);
-  }
-  __syncthreads();
-  if (tid < NCH) {  // per-slot totals
-    uint32_t tot = 0;
-    for (int w = 0; w < kFW; ++w) tot += slot_cnt[tid * kFW + w];
-    tcnt[tid] = tot;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t acc = 0, sstar = NCH - 1, before = 0;
-    for (int s = 0; s < NCH; ++s) {
-      const uint32_t tot = tcnt[s];
-      if (acc + tot >= j) {
-        sstar = (uint32_t)s;
-        before = acc;
-        break;
-      }
-      acc += tot;
-    }
-    sh.bsel[0] = sstar;
-    sh.bsel[1] = before;
-  }
-  __syncthreads();
-  const int sstar = (int)uniform(sh.bsel[0]);
-  const uint32_t jr = j - uniform(sh.bsel[1]);
-  tcnt[tid] = 0u;
-  if (tid < 8) sh.chunk_z[tid] = 0xFFFFFFFFu;
-  __syncthreads();
-  for (uint32_t m = tid; m < nmem; m += kFT) {  // members of slot sstar, per owner row thread
-    const int dl = member_delta(mkey[m], lo, hi);
-    const uint32_t ch = midx[m] >> 3;
-    if (dl && (int)(ch / kFT) == sstar) atomicAdd(&tcnt[ch % kFT], (uint32_t)dl);
-  }
-  __syncthreads();
-  const int chs = sstar * kFT + tid;
-  uint32_t mine = tcnt[tid];
-  if (chs < nchunks) mine += chunk_matches(src[chs], lo, hi);
-  uint32_t tot;
-  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);
-  if (excl < jr && jr <= excl + mine) {
-    sh.bsel[2] = (uint32_t)chs;  // the chunk
-    sh.bsel[3] = jr - excl;      // rank inside it
-  }
-  __syncthreads();
-  const uint32_t cstar = uniform(sh.bsel[2]), need0 = uniform(sh.bsel[3]);
-  for (uint32_t m = tid; m < nmem; m += kFT)
-    if ((midx[m] >> 3) == cstar) sh.chunk_z[midx[m] & 7u] = mkey[m] >> 16;
-  __syncthreads();
-  if (tid == 0) {
-    const uint4 dd = src[min(cstar, (uint32_t)nchunks - 1u)];  // (thread 0 reads the chosen chunk)
-    const uint4 w = make_uint4(key_pair(dd.x), key_pair(dd.y), key_pair(dd.z), key_pair(dd.w));
-    uint32_t need = need0, pick = cstar * 8u;
-    for (uint32_t e = 0; e < 8u; ++e) {
-      const uint32_t zm = sh.chunk_z[e];
-      const uint32_t key = zm != 0xFFFFFFFFu ? zm : chunk_key(w, e);
-      if (key >= lo && key <= hi) {
-        if (need == 1u) {
-          pick = cstar * 8u + e;
-          break;
-        }
-        need -= 1u;
-      }
-    }
-    sh.bsel[4] = pick;
-  }
-  __syncthreads();
-  const uint32_t idx = uniform(sh.bsel[4]);
-  __syncthreads();
-  return idx;
+  return locate_jth<NCH>(sh, nchunks, nmem, lo, hi, j, [&](int s) {
+    const int ch = s * kFT + tid;
+    const uint4 dd = src[ch < nchunks ? ch : nchunks - 1];
+    return make_uint4(key_pair(dd.x), key_pair(dd.y), key_pair(dd.z), key_pair(dd.w));
+  });
 }
 
-// Elements of a chunk (four packed key words) with a key in [lo, hi].
-__device__ __forceinline__ uint32_t chunk_matches_keys(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
-                                                       uint32_t lo, uint32_t hi) {
-  const uint32_t w[4] = {w0, w1, w2, w3};
-  uint32_t n = 0u;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t key = (w[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-    n += (key >= lo && key <= hi) ? 1u : 0u;
-  }
-  return n;
-}
-
-// find_jth_stream on the keys the load pass left in registers: the same
-// ordered search without a second read of the row.
+// The ordered search on the keys the load pass left in registers.
 template <int NCH>
 __device__ __forceinline__ uint32_t find_jth_regs(FastShared &sh, const uint32_t (&k)[NCH][4], int nchunks,
                                                   uint32_t nmem, uint32_t lo, uint32_t hi, uint32_t j) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t *slot_cnt = sh.u32(kOffSlotCnt), *tcnt = sh.u32(kOffTcnt);
-  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  uint32_t *slot_cnt = sh.u32(kOffSlotCnt);
   for (int i = tid; i < NCH * kFW; i += kFT) slot_cnt[i] = 0u;
-  if (tid == 0) sh.bsel[4] = 0u;
   __syncthreads();
   const int ft = fresh_tid();
   static_for<0, NCH>([&](auto S) {
     constexpr int s = decltype(S)::value;
-    const uint32_t n = (s * kFT + ft < nchunks) ? chunk_matches_keys(k[s][0], k[s][1], k[s][2], k[s][3], lo, hi) : 0u;
+    const uint4 w = make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]);
+    const uint32_t n = (s * kFT + ft < nchunks) ? chunk_matches_keys(w, lo, hi) : 0u;
     if (__ballot(n != 0u)) {
       const uint32_t t = wave_sum(n);
       if (lane == 0) atomicAdd(&slot_cnt[s * kFW + wave], t);
     }
   });
-  for (uint32_t m = tid; m < nmem; m += kFT) {
-    const int dl = member_delta(mkey[m], lo, hi);
-    const uint32_t ch = midx[m] >> 3;
-    if (dl) atomicAdd(&slot_cnt[(ch / kFT) * kFW + ((ch % kFT) >> 6)], (uint32_t)dl);
-  }
-  __syncthreads();
-  if (tid < NCH) {  // per-slot totals
-    uint32_t tot = 0;
-    for (int w = 0; w < kFW; ++w) tot += slot_cnt[tid * kFW + w];
-    tcnt[tid] = tot;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t acc = 0, sstar = NCH - 1, before = 0;
-    for (int s = 0; s < NCH; ++s) {
-      const uint32_t tot = tcnt[s];
-      if (acc + tot >= j) {
-        sstar = (uint32_t)s;
-        before = acc;
-        break;
-      }
-      acc += tot;
-    }
-    sh.bsel[0] = sstar;
-    sh.bsel[1] = before;
-  }
-  __syncthreads();
-  const int sstar = (int)uniform(sh.bsel[0]);
-  const uint32_t jr = j - uniform(sh.bsel[1]);
-  tcnt[tid] = 0u;
-  if (tid < 8) sh.chunk_z[tid] = 0xFFFFFFFFu;
-  __syncthreads();
-  for (uint32_t m = tid; m < nmem; m += kFT) {  // members of slot sstar, per owner row thread
-    const int dl = member_delta(mkey[m], lo, hi);
-    const uint32_t ch = midx[m] >> 3;
-    if (dl && (int)(ch / kFT) == sstar) atomicAdd(&tcnt[ch % kFT], (uint32_t)dl);
-  }
-  __syncthreads();
-  // this thread's chunk of slot sstar, selected from the registers
-  uint32_t w0 = 0u, w1 = 0u, w2 = 0u, w3 = 0u;
-  static_for<0, NCH>([&](auto S) {
-    constexpr int s = decltype(S)::value;
-    const bool here = s == sstar;
-    w0 = here ? k[s][0] : w0;
-    w1 = here ? k[s][1] : w1;
-    w2 = here ? k[s][2] : w2;
-    w3 = here ? k[s][3] : w3;
+  return locate_jth<NCH>(sh, nchunks, nmem, lo, hi, j, [&](int sstar) {
+    // this thread's chunk of slot sstar, selected from the registers
+    uint32_t w0 = 0u, w1 = 0u, w2 = 0u, w3 = 0u;
+    static_for<0, NCH>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      const bool here = s == sstar;
+      w0 = here ? k[s][0] : w0;
+      w1 = here ? k[s][1] : w1;
+      w2 = here ? k[s][2] : w2;
+      w3 = here ? k[s][3] : w3;
+    });
+    return make_uint4(w0, w1, w2, w3);
   });
-  const int chs = sstar * kFT + tid;
-  uint32_t mine = tcnt[tid];
-  if (chs < nchunks) mine += chunk_matches_keys(w0, w1, w2, w3, lo, hi);
-  uint32_t tot;
-  const uint32_t excl = block_exclusive_scan<kFW>(mine, sh.uscr, &tot);
-  if (excl < jr && jr <= excl + mine) {
-    sh.bsel[2] = (uint32_t)chs;  // the chunk
-    sh.bsel[3] = jr - excl;      // rank inside it
-  }
-  __syncthreads();
-  const uint32_t cstar = uniform(sh.bsel[2]), need0 = uniform(sh.bsel[3]);
-  for (uint32_t m = tid; m < nmem; m += kFT)
-    if ((midx[m] >> 3) == cstar) sh.chunk_z[midx[m] & 7u] = mkey[m] >> 16;
-  __syncthreads();
-  if ((uint32_t)chs == cstar) {  // the owner of the chunk picks the element
-    const uint4 w = make_uint4(w0, w1, w2, w3);
-    uint32_t need = need0, pick = cstar * 8u;
-    for (uint32_t e = 0; e < 8u; ++e) {
-      const uint32_t zm = sh.chunk_z[e];
-      const uint32_t key = zm != 0xFFFFFFFFu ? zm : chunk_key(w, e);
-      if (key >= lo && key <= hi) {
-        if (need == 1u) {
-          pick = cstar * 8u + e;
-          break;
-        }
-        need -= 1u;
-      }
-    }
-    sh.bsel[4] = pick;
-  }
-  __syncthreads();
-  const uint32_t idx = uniform(sh.bsel[4]);
-  __syncthreads();
-  return idx;
 }
 
 // ---- the full distribution from the window of top keys ----------------------------
