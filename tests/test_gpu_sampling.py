@@ -538,3 +538,37 @@ def test_randomized_rows_every_path():
         rep = compare(run_gpu(w), run_oracle(w))
         _report(f"randomized-{V}", rep)
         assert_parity(rep, f"randomized-{V}")
+
+
+def test_bf16_special_rows_on_the_window_and_mid_paths():
+    """bf16 rows of the fast kernel with +inf, -inf runs, all -inf, and a
+    single finite value, under top-k 0, 100, 1000 and 5000 (the window, the
+    mid-k and the 65536-bin paths decide them) against the oracle."""
+    W = _wl()
+    rng = np.random.default_rng(31)
+    V = 128256
+    rows, ks = [], []
+    for k in (0, 100, 1000, 5000):
+        x = rng.normal(0, 2, V)
+        x[rng.integers(V)] = np.inf                  # invalid distribution
+        rows.append(x)
+        x = rng.normal(0, 2, V)
+        x[rng.choice(V, V // 2, replace=False)] = -np.inf  # half -inf
+        rows.append(x)
+        rows.append(np.full(V, -np.inf))             # all -inf: invalid distribution
+        x = np.full(V, -np.inf)
+        x[rng.integers(V)] = 3.0                     # one finite token
+        rows.append(x)
+        x = np.full(V, 2.0)
+        x[rng.choice(V, 7, replace=False)] = 2.5     # seven maxima over a flat row
+        rows.append(x)
+        ks += [k] * 5
+    B = len(rows)
+    xx = W.f32_to_bf16_bits(np.stack(rows).astype(np.float32))
+    w = _mk(xx, k=np.array(ks, np.int32), p=[0.9 if i % 2 else 1.0 for i in range(B)], u=rng.random(B))
+    print(f"[case] bf16 special rows V={V} B={B}", flush=True)
+    g, r = run_gpu(w), run_oracle(w)
+    rep = compare(g, r)
+    _report("bf16-special", rep)
+    assert_parity(rep, "bf16-special")
+    assert list(r["status"][:5]) == [2, 0, 2, 0, 0], r["status"][:5]
