@@ -6,7 +6,8 @@
 // issued loads and keeps them in registers as 16-bit total-order keys of the
 // RAW logits, two per word: the row is read from memory once.
 //
-// History.  The history ids are requested first.  Inside the load pass,
+// History.  The history ids are requested right after the row's first two
+// slots and the row parameters.  Inside the load pass,
 // after slot kHistAt, they are marked in an LDS bitmap over the vocab; the
 // number of marked tokens before each 32-token bitmap word gives every
 // distinct history token ("member", at most kFastMembers) a dense index in
@@ -32,6 +33,14 @@
 //            from registers) and the members.  Up to 64 candidates are
 //            ranked across the waves and finished by one wave in f64; up to
 //            512 ranked by one thread each; more are sorted in LDS.
+//   window   (top_k = 0 or > kSmallK): a 512-bin LDS histogram of the keys
+//            within 512 of the maximum, every other element's weight summed
+//            in f32 (chunks whose weights are all below e^-37 skipped); the
+//            window's keys carry exact f64 weights and counts for the top-k,
+//            min-p and nucleus cuts and the draw; the chosen token is the
+//            j-th lowest index of its tie group, found in registers.  A cut
+//            or target below a window whose tail still carries mass declines
+//            to the next path.
 //   mid k    (top_k <= kGatherCap): the same bound from the K-th largest
 //            chunk maximum (a cascade of LDS windows), the candidates
 //            gathered from registers and sorted in LDS.
