@@ -57,7 +57,7 @@ extern "C" {
 #define LMRS_ROW_DISTRIBUTION 2 /* non-finite or non-positive weight sum (strategies/mod.rs:39-43) */
 #define LMRS_ROW_PARAM 3        /* a parameter fails its constructor's validation (repetition.rs:57-64,
                                    presence.rs:61-71, temperature.rs:43-50, top_p.rs:26-31,
-                                   min_p.rs:27-29); top_k < 0 */
+                                   min_p.rs:27-29); top_k < -1 */
 #define LMRS_ROW_HISTORY 4      /* history longer than LMRS_MAX_HISTORY for this row */
 /* ... and flag bits above it. */
 #define LMRS_ROW_NEAR_BOUNDARY 0x100 /* the uniform lies within 1e-6 of a CDF boundary of the chosen
@@ -66,6 +66,14 @@ extern "C" {
                                         neighbouring token here; or exp() of a logit at the min-p
                                         cut lies within 1e-12 (relative) of the threshold, where
                                         the host and device exp may round to opposite sides */
+
+/* top_k value that selects the Greedy strategy (greedy.rs:22-29): the first
+ * token in sorted order, log_prob 0, no draw and no other cut, whatever the
+ * values (a NaN or infinite maximum is returned as is).  top_k = 1 is TopK(1)
+ * instead (top_k.rs:39-45): the same token on finite rows, but it draws
+ * through softmax_choice and so reports LMRS_ROW_DISTRIBUTION for a row whose
+ * maximum is +inf, NaN or -inf (strategies/mod.rs:39-43). */
+#define LMRS_GREEDY (-1)
 
 #define LMRS_MAX_VOCAB 262144  /* largest vocab accepted (2^18) */
 #define LMRS_MAX_HISTORY 4096  /* longest per-row history accepted */
@@ -91,7 +99,8 @@ typedef struct lmrs_sample_args {
   const float *presence_penalty;   /* finite; 0 = off together with frequency (presence.rs:102) */
   const float *frequency_penalty;  /* finite */
   const double *temperature;       /* finite, > 0; 1.0 = off (temperature.rs:68) */
-  const int32_t *top_k;            /* >= 0; 0 = off, 1 = greedy */
+  const int32_t *top_k;            /* 0 = off; k > 0 = TopK(k) (top_k.rs:39-45); LMRS_GREEDY = Greedy
+                                      (greedy.rs:22-29); below LMRS_GREEDY: LMRS_ROW_PARAM */
   const double *top_p;             /* in (0, 1]; 1.0 = off */
   const double *uniforms;          /* in [0, 1): the draw's uniform (next_unit of the reference's
                                       LCG, strategies/mod.rs:57-61, or any caller RNG).  Required
@@ -113,8 +122,8 @@ typedef struct lmrs_sample_args {
  * batch).  Asynchronous on `stream`.  Returns LMRS_OK or an LMRS_ERR_* code;
  * per-row problems are reported in status[r] and never fail the call.
  *
- * Per row: the processors, then top_k == 1 is Greedy (no other strategy
- * parameter applies); otherwise the candidates are cut by top-k (top_k.rs:39-45),
+ * Per row: the processors, then top_k == LMRS_GREEDY is Greedy (no other
+ * strategy parameter applies); otherwise the candidates are cut by top-k (top_k.rs:39-45),
  * then by min-p (min_p.rs:45-53), then by the nucleus (top_p.rs:45-58), and
  * softmax_choice draws from what is left (strategies/mod.rs:27-55).  Each cut
  * that is off keeps everything, so a row with one strategy parameter set is

@@ -1241,7 +1241,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   const uint4 *src2 = fresh(src);  // the re-reads
   SelState &ss = sh.ss();
 
-  if (k_on && c.top_k <= kSmallK) {  // ---- greedy and small k ----------------------
+  if (c.greedy || (k_on && c.top_k <= kSmallK)) {  // ---- greedy and small k ----------
     // Greedy (greedy.rs:22-29) is the case k = 1: the first of the sorted candidates.
     const uint32_t K = (uint32_t)c.top_k;
     uint32_t L = tvhi;
@@ -1313,7 +1313,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
         if ((uint32_t)tid >= ncand) rank = (uint32_t)tid;
         const uint32_t lo32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)g);
         const uint32_t hi32 = (uint32_t)__builtin_amdgcn_ds_permute((int)(rank * 4u), (int)(uint32_t)(g >> 32));
-        finish_wave<TR>(((uint64_t)hi32 << 32) | lo32, c, a, r, K, K == 1u);
+        finish_wave<TR>(((uint64_t)hi32 << 32) | lo32, c, a, r, K, c.greedy);
       }
       return true;
     }
@@ -1329,7 +1329,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
         if (rank < 64u) sorted[rank] = g;
       }
       __syncthreads();
-      if (tid < 64) finish_wave<TR>((uint32_t)tid < ncand ? sorted[tid] : ~0ull, c, a, r, K, K == 1u);
+      if (tid < 64) finish_wave<TR>((uint32_t)tid < ncand ? sorted[tid] : ~0ull, c, a, r, K, c.greedy);
       return true;
     }
     sort_gather<kFT>(ss, ncand);

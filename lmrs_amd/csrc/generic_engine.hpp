@@ -355,6 +355,10 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
   // Thread t owns sorted entries P*t .. P*t+P-1 of the first k.
   constexpr int P = kGatherCap / NT, NW = NT / 64;
   const float M = TR::value(~uniform((uint32_t)(ss.gather[0] >> 32)));
+  if (c.greedy) {  // Greedy (greedy.rs:22-29): the first sorted candidate, no distribution
+    if (threadIdx.x == 0) write_row(a, r, (uint32_t)(ss.gather[0] & 0xFFFFFFFFu), 0.0f, M, LMRS_ROW_OK);
+    return;
+  }
   int32_t flags = 0;
   if (c.min_p >= 0.0) {  // the min-p cut (min_p.rs:45-53): a prefix of the k candidates
     const double thr = minp_threshold(M, c);
@@ -483,7 +487,7 @@ __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const R
                                            uint32_t kmax, uint32_t imax, uint32_t nneg) {
   using TR = typename Row::TR;
   const float M = TR::value(kmax);
-  if (c.top_k == 1) {  // Greedy (greedy.rs:22-29): sorted[0], log_prob 0
+  if (c.greedy) {  // Greedy (greedy.rs:22-29): sorted[0], log_prob 0
     if (threadIdx.x == 0) write_row(a, r, imax, 0.0f, M, LMRS_ROW_OK);
     return;
   }

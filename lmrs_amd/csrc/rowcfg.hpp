@@ -21,6 +21,7 @@ constexpr int kBitmapWords = LMRS_MAX_VOCAB / 32;
 struct RowCfg {
   int status;          // LMRS_ROW_OK or an error code decided before sampling
   int rep_on, pres_on, temp_on, hist_on;
+  int greedy;          // Greedy (top_k == LMRS_GREEDY): sorted[0], no distribution
   float pf, nf;        // repetition factors (bf16-rounded for bf16 rows)
   float presence, frequency;
   float scale;         // (float)(1.0 / T)
@@ -65,6 +66,7 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
   c.pres_on = uniform((int32_t)s.pres_on);
   c.temp_on = uniform((int32_t)s.temp_on);
   c.hist_on = uniform((int32_t)s.hist_on);
+  c.greedy = uniform((int32_t)s.greedy);
   c.pf = uniform(s.pf);
   c.nf = uniform(s.nf);
   c.presence = uniform(s.presence);
@@ -83,7 +85,8 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
 // mirrors the constructors: RepetitionPenalty::new (repetition.rs:57-64),
 // FrequencyPresencePenalty::new (presence.rs:61-71), Temperature::new
 // (temperature.rs:43-50), TopP::new (top_p.rs:26-31), MinP::new
-// (min_p.rs:27-29, a negative value switching the cut off); top_k < 0 invalid.
+// (min_p.rs:27-29, a negative value switching the cut off); top_k below
+// LMRS_GREEDY invalid.  Greedy rows carry top_k = 1 with `greedy` set.
 __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype) {
   RowCfg c;
   c.status = LMRS_ROW_OK;
@@ -96,7 +99,7 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   double mp = a.min_p ? a.min_p[r] : -1.0;
   c.u = a.uniforms ? a.uniforms[r] : 0.0;
   if (!(__builtin_isfinite(rep) && rep > 0.0f) || !__builtin_isfinite(pres) ||
-      !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < 0 ||
+      !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < LMRS_GREEDY ||
       !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0) || __builtin_isnan(mp) || mp > 1.0)
     c.status = LMRS_ROW_PARAM;
   c.h_begin = 0;
@@ -123,7 +126,8 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   c.presence = pres;
   c.frequency = freq;
   c.scale = (float)(1.0 / t);                                  // temperature.rs:71
-  c.top_k = k;
+  c.greedy = k == LMRS_GREEDY;
+  c.top_k = c.greedy ? 1 : k;
   c.top_p = p;
   c.min_p = mp < 0.0 ? -1.0 : mp;
   return c;

@@ -25,6 +25,7 @@ LMRS_OK = 0
 ERR_NULL_ARGUMENT, ERR_BAD_DTYPE, ERR_BAD_SHAPE, ERR_LAUNCH, ERR_ALIGNMENT = -1, -2, -3, -4, -5
 ROW_OK, ROW_EMPTY, ROW_DISTRIBUTION, ROW_PARAM, ROW_HISTORY = 0, 1, 2, 3, 4
 ROW_NEAR_BOUNDARY = 0x100
+GREEDY = -1  # top_k value selecting Greedy (greedy.rs:22-29); top_k = 1 is TopK(1)
 MAX_VOCAB = 262144
 MAX_HISTORY = 4096
 
@@ -251,16 +252,16 @@ class SamplingStrategy:
 
 
 class Greedy(SamplingStrategy):
-    """Greedy (strategies/greedy.rs:19-29)."""
+    """Greedy (strategies/greedy.rs:19-29): sorted[0], no draw, no distribution check."""
 
-    top_k = 1
+    top_k = GREEDY
     stochastic = False
 
 
 class BeamSearch(SamplingStrategy):
-    """BeamSearch (strategies/beam.rs:23-50): the first sorted candidate."""
+    """BeamSearch (strategies/beam.rs:23-50): the first sorted candidate, as Greedy."""
 
-    top_k = 1
+    top_k = GREEDY
     stochastic = False
 
     def __init__(self, width: int):

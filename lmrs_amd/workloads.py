@@ -143,12 +143,13 @@ def c3(seed: int = BASE_SEED + 3, batch: int = 256, vocab: int = 128256, hist: i
 
 
 def c4(seed: int = BASE_SEED + 4, batch: int = 1024, vocab: int = 151936, layout: str = "alternate") -> Workload:
-    """Large batch: bf16 N(0,3^2); half greedy (k=1), half full multinomial (k=0, p=1, T=1)."""
+    """Large batch: bf16 N(0,3^2); half Greedy (top_k = -1, the kernel's Greedy code), half full
+    multinomial (k=0, p=1, T=1)."""
     rng = np.random.default_rng(seed)
     x = (rng.standard_normal((batch, vocab)) * 3.0).astype(np.float32)
     rep, pres, freq, t, k, p = _params(batch)
     greedy = (np.arange(batch) % 2 == 0) if layout == "alternate" else (np.arange(batch) < batch // 2)
-    k[greedy] = 1
+    k[greedy] = -1  # Greedy
     return Workload("C4", f32_to_bf16_bits(x), rep, pres, freq, t, k, p, row_uniforms(batch, seed),
                     notes={"layout": layout})
 

@@ -393,7 +393,7 @@ int lmrs_oracle_sample_row(const void *logits, int dtype, int64_t n, const uint3
   if (dtype != 0 && dtype != 2) return LMRS_ORACLE_ERR_PARAM;
   if (!valid_repetition(pr->repetition_penalty) ||
       !valid_presence(pr->presence_penalty, pr->frequency_penalty) ||
-      !valid_temperature(pr->temperature) || pr->top_k < 0 || !isfinite(pr->top_p) ||
+      !valid_temperature(pr->temperature) || pr->top_k < -1 || !isfinite(pr->top_p) ||
       pr->top_p <= 0.0 || pr->top_p > 1.0 || isnan(pr->min_p) || pr->min_p > 1.0)
     return LMRS_ORACLE_ERR_PARAM; /* min_p: min_p.rs:27-29, negative = off */
   if (diag) {
@@ -420,7 +420,9 @@ int lmrs_oracle_sample_row(const void *logits, int dtype, int64_t n, const uint3
   int st;
   if (n <= 0) {
     st = LMRS_ORACLE_ERR_EMPTY;
-  } else if (pr->top_k == 1) {
+  } else if (pr->top_k == -1) {
+    /* Greedy (greedy.rs:22-29): sorted[0] whatever its value; TopK(1) below
+       goes through softmax_choice and rejects a non-finite maximum */
     st = lmrs_oracle_greedy(v, n, out);
     if (diag) {
       diag->n_candidates = 1;

@@ -95,7 +95,7 @@ typedef struct {
   float presence_penalty;   /* 0.0 = off (with frequency 0) */
   float frequency_penalty;
   double temperature;       /* 1.0 = off */
-  int64_t top_k;            /* 0 = off */
+  int64_t top_k;            /* 0 = off, -1 = Greedy, k > 0 = TopK(k) */
   double top_p;             /* >= 1.0 = off; must be in (0, 1] */
   double min_p;             /* < 0 = off; else must be in [0, 1] */
 } lmrs_oracle_params;
@@ -126,7 +126,10 @@ typedef struct {
  * the inverse-CDF draw with the caller's uniform u), built from reference
  * primitives:
  * processors as in Sampler::sample (sampler.rs:178-186), strategies as in
- * the strategies/ files.  top_k == 1 is Greedy (greedy.rs:22-29).
+ * the strategies/ files.  top_k == -1 is Greedy (greedy.rs:22-29), which
+ * ignores the other cuts; top_k == 1 is TopK(1) (top_k.rs:39-45), which
+ * draws through softmax_choice and so reports an invalid distribution for a
+ * row whose maximum is not finite.
  * logits: one row, dtype 0 (bf16 bits) or 2 (f32); not modified.
  * processed_out (optional, n floats): the processed row as f32. */
 int lmrs_oracle_sample_row(const void *logits, int dtype, int64_t n,

@@ -16,6 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblmrs_oracle.so")
 
 OK, ERR_EMPTY, ERR_DISTRIBUTION, ERR_PARAM = 0, 1, 2, 3
+GREEDY = -1  # top_k value that selects Greedy (greedy.rs:22-29); top_k = 1 is TopK(1)
 
 
 class Output(ctypes.Structure):

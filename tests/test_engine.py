@@ -20,7 +20,8 @@ def test_generation_config_validation_and_default():
 def test_sampler_for_mapping():
     assert E.sampler_for(E.GenerationConfig(top_k=40, top_p=0.5)) == E.RowParams(40, 1.0, 1.0, True)  # top_k wins
     assert E.sampler_for(E.GenerationConfig(top_p=0.9, temperature=0.7)) == E.RowParams(0, 0.9, 0.7, True)
-    assert E.sampler_for(E.GenerationConfig()) == E.RowParams(1, 1.0, 1.0, False)  # Greedy
+    assert E.sampler_for(E.GenerationConfig()) == E.RowParams(S.GREEDY, 1.0, 1.0, False)  # Greedy
+    assert E.sampler_for(E.GenerationConfig(top_k=1)) == E.RowParams(1, 1.0, 1.0, True)  # TopK(1) draws
     with pytest.raises(S.SamplingError):
         E.sampler_for(E.GenerationConfig(top_k=0))  # TopK::new(0)
     with pytest.raises(S.SamplingError):

@@ -61,9 +61,10 @@ def test_config_parity(cfg, rows):
 def test_c1_greedy_check():
     W = _wl()
     w = W.c1(batch=2)
-    w.top_k[:] = 1
-    rep = compare(run_gpu(w), run_oracle(w))
-    assert_parity(rep, "C1-greedy")
+    for k in (-1, 1):  # Greedy, and TopK(1), its softmax_choice twin
+        w.top_k[:] = k
+        rep = compare(run_gpu(w), run_oracle(w))
+        assert_parity(rep, f"C1-greedy k={k}")
 
 
 def test_c4_contiguous_halves():
@@ -226,9 +227,9 @@ def test_special_values_and_statuses():
     from lmrs_amd import sampling as S
 
     V = 16
-    x = np.zeros((8, V), np.float32)
+    x = np.zeros((12, V), np.float32)
     x[0, 3] = np.nan                      # NaN row, sampled -> invalid distribution
-    x[1, 3] = np.nan                      # NaN row, greedy -> the NaN's index
+    x[1, 3] = np.nan                      # NaN row, Greedy -> the NaN's index
     x[2, 5] = np.inf                      # +inf -> invalid distribution
     x[3, :] = -np.inf                     # all -inf -> invalid distribution
     x[4, :] = -np.inf
@@ -237,13 +238,17 @@ def test_special_values_and_statuses():
     x[6, :] = -0.0
     x[6, 2] = 0.0                         # +0 sorts above -0
     x[7, :] = np.linspace(0, 1, V)
-    k = np.array([0, 1, 0, 0, 0, 0, 1, 0], np.int32)
-    p = np.array([1.0, 1.0, 1.0, 1.0, 0.5, 1.0, 1.0, 1.0])
-    t = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 0.0, 1.0, 1.0])   # row 5: invalid temperature
-    w = _mk(x, k=k, p=p, t=t, u=np.full(8, 0.7))
+    x[8, 5] = np.inf                      # TopK(1) (top_k.rs:39-45) of a +inf maximum: invalid
+    x[9, 3] = np.nan                      # TopK(1) of a NaN row: invalid
+    x[10, :] = -np.inf                    # TopK(1) of an all -inf row: invalid
+    x[11, :] = -np.inf                    # Greedy of an all -inf row: token 0
+    k = np.array([0, -1, 0, 0, 0, 0, 1, 0, 1, 1, 1, -1], np.int32)
+    p = np.array([1.0, 1.0, 1.0, 1.0, 0.5, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0])
+    t = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 0.0, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0])   # row 5: invalid temperature
+    w = _mk(x, k=k, p=p, t=t, u=np.full(12, 0.7))
     g, r = run_gpu(w), run_oracle(w)
     assert list(g["status"] & 0xFF) == list(r["status"]), (g["status"], r["status"])
-    assert list(r["status"]) == [2, 0, 2, 2, 0, 3, 0, 0]
+    assert list(r["status"]) == [2, 0, 2, 2, 0, 3, 0, 0, 2, 2, 2, 0]
     ok = r["status"] == 0
     assert np.array_equal(g["token_id"][ok], r["token_id"][ok])
     # empty vocab
@@ -362,10 +367,10 @@ def test_small_k_bound_and_candidate_paths():
                     top = np.argsort(-x)[:200]
                     h = list((top + rng.integers(-3, 4, 200)).clip(0, V - 1)) + list(rng.integers(0, V, 500))
                     k, t = 40, 0.7
-                else:  # greedy with a penalised maximum
+                else:  # Greedy and TopK(1) with a penalised maximum
                     top = int(np.argmax(x))
                     h = [top] * 3 + list(rng.integers(0, V, 100))
-                    k = 1
+                    k = -1 if len(rows) % 2 else 1
                 rows.append(x)
                 ks.append(k)
                 hists.append(h)
@@ -524,7 +529,7 @@ def test_randomized_rows_every_path():
             else:
                 x = rng.gumbel(0, 2.0, V)
             rows.append(x.astype(np.float32))
-            ks.append(int(rng.choice([0, 0, 1, 2, 10, 50, 64, 65, 300, 1000, 4096, 5000, V + 3])))
+            ks.append(int(rng.choice([0, 0, -1, 1, 2, 10, 50, 64, 65, 300, 1000, 4096, 5000, V + 3])))
             ps.append(float(rng.choice([1.0, 1.0, rng.uniform(0.05, 1.0), 0.999])))
             mps.append(float(rng.choice([-1.0, -1.0, -1.0, 0.0, rng.uniform(0, 0.5), 10 ** rng.uniform(-12, -1)])))
             ts.append(float(rng.choice([1.0, 1.0, rng.uniform(0.3, 2.5)])))

@@ -84,7 +84,7 @@ def test_reference_stochastic_exact_ids():
 
 def test_reference_sampler_default_bf16():
     for v in VEC["sampler_default_bf16"]:
-        st, (tok, lp, logit), _, _ = O.sample_row(bf(v["logits"]), None, O.make_params(top_k=1), 0.0)
+        st, (tok, lp, logit), _, _ = O.sample_row(bf(v["logits"]), None, O.make_params(top_k=O.GREEDY), 0.0)
         assert st == O.OK and tok == v["token"] and lp == 0.0
 
 
@@ -120,7 +120,7 @@ def test_reference_validation():
     assert O.sample_row(x, None, O.make_params(temperature=0.0), 0.5)[0] == O.ERR_PARAM
     assert O.sample_row(x, None, O.make_params(top_p=0.0), 0.5)[0] == O.ERR_PARAM
     assert O.sample_row(x, None, O.make_params(top_p=1.5), 0.5)[0] == O.ERR_PARAM
-    assert O.sample_row(x, None, O.make_params(top_k=-1), 0.5)[0] == O.ERR_PARAM
+    assert O.sample_row(x, None, O.make_params(top_k=-2), 0.5)[0] == O.ERR_PARAM
     assert O.top_k([1.0], 0, 1)[0] == O.ERR_PARAM
 
 
@@ -130,7 +130,7 @@ def test_reference_engine_one_hot_greedy():
     for t in v["script"]:
         row = np.zeros(v["vocab"], np.float32)
         row[t] = v["hot_value"]
-        got.append(O.sample_row(torch_bf16_bits(row), None, O.make_params(top_k=1), 0.0)[1][0])
+        got.append(O.sample_row(torch_bf16_bits(row), None, O.make_params(top_k=O.GREEDY), 0.0)[1][0])
     assert got == v["tokens"]
 
 
@@ -300,7 +300,9 @@ def test_composition_reduces_to_reference_strategies():
         r = O.sample_row(x, None, O.make_params(min_p=mp), u)
         assert r[0] == st_m and r[1] == m
         _, g = O.greedy(x)
-        assert O.sample_row(x, None, O.make_params(top_k=1), u)[1] == g
+        assert O.sample_row(x, None, O.make_params(top_k=O.GREEDY), u)[1] == g
+        _, g1, _ = O.top_k(x, 1, seed)
+        assert O.sample_row(x, None, O.make_params(top_k=1), u)[1] == g1
         # no filter: full multinomial == TopK(n)
         _, f, _ = O.top_k(x, n, seed)
         assert O.sample_row(x, None, O.make_params(), u)[1] == f
@@ -381,7 +383,7 @@ def test_min_p_special_values_and_validation():
     for off in (-0.5, -np.inf):
         assert O.sample_row(f(1.0, 0.0), None, P(min_p=off), 0.6)[1] == O.sample_row(f(1.0, 0.0), None, P(), 0.6)[1]
     # greedy ignores min-p
-    assert O.sample_row(f(1.0, np.nan), None, P(top_k=1, min_p=0.5), 0.3)[1][0] == 1
+    assert O.sample_row(f(1.0, np.nan), None, P(top_k=O.GREEDY, min_p=0.5), 0.3)[1][0] == 1
 
 
 def test_top_k_one_is_greedy_and_k_ge_v_is_full():
@@ -389,6 +391,7 @@ def test_top_k_one_is_greedy_and_k_ge_v_is_full():
     x = rng.choice(np.array([1.0, 2.0, 2.0, 0.5], np.float32), size=50)
     for u in (0.0, 0.3, 0.999):
         assert O.sample_row(x, None, O.make_params(top_k=1), u)[1][0] == int(np.argmax(x))
+        assert O.sample_row(x, None, O.make_params(top_k=O.GREEDY), u)[1][0] == int(np.argmax(x))
         assert O.sample_row(x, None, O.make_params(top_k=50), u)[1] == O.sample_row(x, None, O.make_params(), u)[1]
         assert O.sample_row(x, None, O.make_params(top_k=500), u)[1] == O.sample_row(x, None, O.make_params(), u)[1]
 
@@ -523,9 +526,30 @@ def test_invalid_distribution_rows():
     infrow = np.array([1.0, np.inf, 0.5], np.float32)
     assert O.sample_row(infrow, None, O.make_params(), 0.3)[0] == O.ERR_DISTRIBUTION
     # greedy does not compute weights: the NaN (sorted first) is returned
-    assert O.sample_row(nanrow, None, O.make_params(top_k=1), 0.3)[1][0] == 1
+    assert O.sample_row(nanrow, None, O.make_params(top_k=O.GREEDY), 0.3)[1][0] == 1
     neginf = np.array([-np.inf, -np.inf], np.float32)
     assert O.sample_row(neginf, None, O.make_params(), 0.3)[0] == O.ERR_DISTRIBUTION
     # -inf below the top-k cut does not matter
     mixed = np.array([1.0, -np.inf, 0.0], np.float32)
     assert O.sample_row(mixed, None, O.make_params(), 0.999)[0] == O.OK
+
+
+def test_top_k_one_is_not_greedy_on_non_finite_rows():
+    # TopK(1) draws through softmax_choice (top_k.rs:39-45): a +inf, NaN or
+    # all -inf maximum gives the invalid-distribution error and consumes no
+    # draw, where Greedy (greedy.rs:22-29) returns the first sorted token
+    rows = [np.array([np.inf, 1.0, 0.0], np.float32), np.array([1.0, np.nan, 0.5], np.float32),
+            np.array([-np.inf, -np.inf, -np.inf], np.float32), np.array([0.5, np.inf, np.inf], np.float32)]
+    for x in rows:
+        st_ref, _, state = O.top_k(x, 1, 42)
+        assert st_ref == O.ERR_DISTRIBUTION and state == 42  # no draw consumed
+        assert O.sample_row(x, None, O.make_params(top_k=1), 0.3)[0] == O.ERR_DISTRIBUTION
+        st_g, g = O.greedy(x)
+        assert st_g == O.OK
+        r = O.sample_row(x, None, O.make_params(top_k=O.GREEDY), 0.3)
+        assert r[0] == O.OK and r[1][0] == g[0] and r[1][1] == 0.0
+    # finite rows: the same token, log_prob 0 either way
+    x = np.array([0.5, 2.0, 2.0, -1.0], np.float32)
+    a = O.sample_row(x, None, O.make_params(top_k=1), 0.7)
+    b = O.sample_row(x, None, O.make_params(top_k=O.GREEDY), 0.7)
+    assert a[0] == b[0] == O.OK and a[1] == b[1] and a[1][0] == 1 and a[1][1] == 0.0
