@@ -228,17 +228,14 @@ __device__ __forceinline__ uint32_t penalise_member(uint32_t raw, uint32_t count
   return __float_as_uint(v) >> 16;
 }
 
-// LDS arena with phase-dependent views (byte offsets):
-//   [0, 64K)      history hash: token + 1, multiplicity | raw key << 16
-//                 (history build); then SelState [0, 57K): gather list, sort
-//                 and finish scratch
-//                 [60K, 64K): window histogram of the count cascade
-//   [64K, 84K)    membership bitmap over the vocab
-//   [136K, 152K)  member list: token ids, raw key | z key << 16
-//   full path: [0, 128K) 65536 16-bit counters; after compaction [128K, 152K)
-//   the entries (key << 16 | count) and [0, 72K) their prefixes; for the
-//   final search the member list is rebuilt and [128K, 134K) holds the
-// LDS arena with phase-dependent views (byte offsets):
+// LDS arena with phase-dependent views (byte offsets).  The lean pass of
+// greedy and small-k rows (lean_row):
+//   [0, 32K)      history hash: token + 1 | multiplicity << 18
+//   [32K, 42K)    per wave, the chunks it recorded: raw words, chunk index
+//   [44K, 59K)    per wave, its candidates (y key << 32 | index); the count
+//                 histogram over y keys from the bound; the finishing wave's
+//                 group table and index scratch
+// The general pass of every other row (and of a lean row that declines):
 //   [0, 10K)      per bitmap word, the number of members before it (history
 //                 build); then [0, 57K) SelState: candidate list, sort and
 //                 finish scratch
@@ -265,6 +262,26 @@ constexpr int kOffMembers = 128 * 1024;
 constexpr int kOffEntries = 128 * 1024;
 constexpr int kOffSlotCnt = 0;
 constexpr int kOffTcnt = kMaxSlots * kFW * 4;
+constexpr int kLOffHash = 0;             // lean pass: history hash
+constexpr int kLHashBits = 13;
+constexpr int kLHashSlots = 1 << kLHashBits;
+constexpr int kRecSeg = 64;              // chunks a wave records
+constexpr int kLOffRecRaw = 32 * 1024;
+constexpr int kLOffRecCh = kLOffRecRaw + kFW * kRecSeg * 16;
+constexpr int kLOffBinMin = kLOffRecCh + kFW * kRecSeg * 4;  // per candidate bin, its lowest index
+constexpr int kOffCand = 44 * 1024;      // candidate list, one segment per wave
+constexpr int kCandSeg = 128;            // entries of a wave's segment
+constexpr int kOffCandHist = kOffCand + kFW * kCandSeg * 8;
+constexpr int kCandBins = 512;           // y keys y0 .. y0 + 510, then one bin for everything above
+constexpr int kOffGroups = kOffCandHist + kCandBins * 4;
+constexpr int kOffMatch = kOffGroups + 64 * 8;
+constexpr int kCtrLeanBad = 6;           // counters() words of the lean pass: a reason to decline,
+constexpr int kCtrLeanYmax = 7;          // and the largest listed y key
+constexpr int kLOffWbin = 64 * 1024;     // lean pass: exp(y - y0) of each candidate bin (f64)
+static_assert(kLOffHash + kLHashSlots * 4 <= kLOffRecRaw && kLOffBinMin + kCandBins * 4 <= kOffCand, "lean views");
+static_assert(kOffMatch + kFW * kCandSeg * 4 <= kOffWhist, "candidate views");
+static_assert(LMRS_MAX_HISTORY * 2 <= kLHashSlots && kFastMaxVocab < (1 << 18) && LMRS_MAX_HISTORY < (1 << 14),
+              "hash load and packing");
 static_assert(kOffPrefix + kMaxWords * 2 <= kOffWhist, "prefix view");
 static_assert((int)sizeof(SelState) <= kOffWhist, "SelState view");
 static_assert(kOffWhist + kMaxWindow * 4 <= kOffCounters && kTvBins <= kMaxWindow, "window view");
@@ -287,6 +304,8 @@ struct FastShared {
   int32_t iscr[kWaves];
   uint32_t chunk_z[8];
   uint32_t bsel[8];
+  int32_t lean_l[kFW];      // lean pass: each wave's bound
+  uint32_t cand_n[kFW];     // candidates listed by each wave
 
   __device__ uint32_t *u32(int off) { return (uint32_t *)(arena + off); }
   __device__ uint32_t *m_idx() { return u32(kOffMembers); }
@@ -1096,6 +1115,468 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   return true;
 }
 
+// The j-th (1-based) lowest index among the candidates whose y key is yk
+// (one wave; j at most their number).  Wave w listed cand_n[w] candidates
+// at entries w kCandSeg ... of the list.
+__device__ __forceinline__ uint32_t stream_nth_index(FastShared &sh, uint32_t yk, uint32_t j) {
+  const uint32_t lane = threadIdx.x & 63u;
+  uint32_t cn[kFW];
+#pragma unroll
+  for (int w = 0; w < kFW; ++w) cn[w] = uniform(sh.cand_n[w]);
+  const uint64_t *cand = (const uint64_t *)sh.u32(kOffCand);
+  uint32_t *mt = sh.u32(kOffMatch);
+  uint32_t m = 0u;
+#pragma unroll
+  for (int w = 0; w < kFW; ++w) {
+    for (uint32_t b = 0u; b < cn[w]; b += 64u) {
+      const uint32_t i = b + lane;
+      const uint64_t e = i < cn[w] ? cand[w * kCandSeg + i] : ~0ull;
+      const bool hit = i < cn[w] && (uint32_t)(e >> 32) == yk;
+      const uint64_t mask = __ballot(hit);
+      if (hit)
+        mt[m + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u))] =
+            (uint32_t)e;
+      m += (uint32_t)__builtin_popcountll(mask);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the wave's LDS writes before its reads
+  if (m <= 64u) {  // rank among at most 64, one per lane
+    const uint32_t v = lane < m ? mt[lane] : 0xFFFFFFFFu;
+    uint32_t rank = 0u;
+    for (uint32_t q = 0u; q < m; ++q) rank += (uint32_t)__builtin_amdgcn_readlane((int)v, (int)q) < v ? 1u : 0u;
+    const uint64_t pick = __ballot(lane < m && rank + 1u == j);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, pick ? (int)__builtin_ctzll(pick) : 0);
+  }
+  // the smallest x with at least j indices <= x, one bit at a time
+  uint32_t res = 0u;
+  for (int bit = 17; bit >= 0; --bit) {
+    const uint32_t t = res | (1u << bit);
+    uint32_t below = 0u;
+    for (uint32_t q = lane; q < m; q += 64u) below += mt[q] < t ? 1u : 0u;
+    if (wave_sum(below) < j) res = t;
+  }
+  return res;
+}
+
+// Finishes a greedy or small-k row from its listed candidates: every element
+// whose y key is at least y0, in per-wave segments (cand_n), with their y
+// keys counted in the histogram from y0, the lowest index of each bin in
+// binmin, the largest key in counters()[kCtrLeanYmax] and each bin's weight
+// exp(y - y0) in wbin (every wave enters, after a barrier).  Every wave reads
+// the bins below the largest key, 64 at a time, one per lane, and finds the
+// group (y key) of the K-th token; one wave finishes from the groups in
+// descending y:
+// weights times counts, the min-p and nucleus cuts and the draw
+// (softmax_choice, strategies/mod.rs:27-55), and the chosen token, the j-th
+// lowest index among the candidates of its group -- the reference's order
+// (value descending, index ascending, strategies/mod.rs:21-25), since the
+// tokens of a group share their weight.  The weights are the reference's
+// exp(y - max) times exp(max - y0): the cuts and the draw compare ratios of
+// sums, which that common factor leaves as they are (up to the last bit).
+// Returns false (uniformly, with nothing written) when a flag is set (a NaN,
+// an overflowed segment), fewer than K tokens lie in the 256 bins below the
+// largest key, the
+// largest key lies above the bins or more than 700 above y0 in value (its
+// weight would near the f64 range; the general pass also takes the rows the
+// reference rejects for a non-finite maximum), or the K-th
+// token is in the lowest listed group while that group may continue below
+// the listed keys (tie_below).
+__device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_args &a, int r, const RowCfg &c,
+                                              uint32_t K, uint32_t y0, bool tie_below) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t ymax = uniform(sh.counters()[kCtrLeanYmax]);
+  if (uniform(sh.counters()[kCtrLeanBad]) != 0u || ymax < y0) return false;
+  const uint32_t bmax = ymax - y0;
+  if (bmax >= (uint32_t)kCandBins - 1u) return false;  // the largest candidates lie above the bins
+  // weights up to e^700 keep every sum of at most kCandCap of them finite
+  if (!(key16_value(ymax) - key16_value(y0) <= 700.0f)) return false;
+  // Rounds of 64 bins in descending y keys (lane l of round e: bin bmax - l -
+  // 64 e) until the count reaches K; the non-empty bins down to the K-th
+  // token's go, in order, to lanes 0 .. G - 1 (G <= K <= 64: one token each
+  // at least) as bin << 20 | count.
+  const uint32_t *hb = sh.u32(kOffCandHist);
+  uint32_t base = 0u, G = 0u, keep_k = 0u, packed = 0u;
+  bool found = false;
+  for (int e = 0; e < 4 && !found; ++e) {
+    const int bl = (int)bmax - (int)lane - 64 * e;
+    const uint32_t cnt = bl >= 0 ? hb[bl] : 0u;
+    const uint32_t incl = wave_inclusive<OpSum>(cnt, 0u) + base;
+    const uint64_t reach = __ballot(incl >= K);
+    const uint32_t lim = reach ? (uint32_t)__builtin_ctzll(reach) : 63u;  // lanes within the cut
+    const bool ne = cnt != 0u && lane <= lim;
+    const uint64_t nzm = __ballot(ne), zm = ~nzm;
+    const uint32_t n = (uint32_t)__builtin_popcountll(nzm);
+    // a permutation of the lanes: the bins to G .. G + n - 1, the others around them
+    const uint32_t d = __builtin_amdgcn_mbcnt_hi((uint32_t)(zm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)zm, 0u));
+    const uint32_t dest = ne ? G + __builtin_amdgcn_mbcnt_hi((uint32_t)(nzm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)nzm, 0u))
+                             : (d < G ? d : d + n);
+    packed |= (uint32_t)__builtin_amdgcn_ds_permute((int)(dest * 4u), (int)(ne ? (((uint32_t)bl << 20) | cnt) : 0u));
+    G += n;
+    if (reach) {
+      found = true;
+      keep_k = K - ((uint32_t)__builtin_amdgcn_readlane((int)incl, (int)lim) -
+                    (uint32_t)__builtin_amdgcn_readlane((int)cnt, (int)lim));
+      // the K-th token in the lowest listed bin, which may continue below za
+      if (tie_below && bmax == lim + 64u * (uint32_t)e) return false;
+    } else {
+      base = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+    }
+  }
+  if (!found) return false;
+  if (threadIdx.x >= 64u) return true;  // one wave finishes the row
+  const bool in = lane < G;
+  const uint32_t gb = in ? packed >> 20 : 0u;                       // the group's bin (y key - y0)
+  const uint32_t yk = y0 + gb;
+  const uint32_t gcnt = lane + 1u == G ? keep_k : (packed & 0xFFFFFu);  // the K-th token's group keeps keep_k
+  const uint32_t *binmin = sh.u32(kLOffBinMin);
+  const float M = key16_value(ymax);
+  if (c.greedy) {  // Greedy (greedy.rs:22-29): the lowest index at the maximum, log_prob 0
+    const uint32_t tok = uniform(binmin[bmax]);
+    if (lane == 0u) write_row(a, r, tok, 0.0f, M, LMRS_ROW_OK);
+    return true;
+  }
+  const double w = in ? ((const double *)sh.u32(kLOffWbin))[gb] : 0.0;  // exp(y - y0) per token
+  const double rw = in ? 1.0 / w : 0.0;
+  const double incm = wave_inclusive<OpSum>(w * (double)gcnt, 0.0);
+  const double excl = incm - w * (double)gcnt;
+  auto at = [](double v, uint32_t l) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, (int)l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), (int)l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+  };
+  uint32_t last = G - 1u, last_keep = keep_k;  // the last kept group, and its kept tokens
+  double cand_mass = at(incm, last);
+  int32_t flags = 0;
+  if (c.min_p >= 0.0) {  // the min-p cut (min_p.rs:45-53): a prefix of the groups
+    const double thr = minp_threshold(M, c);
+    if (!(thr == thr)) {  // NaN threshold: softmax_choice of nothing (strategies/mod.rs:28-30)
+      if (lane == 0u) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    const uint32_t ymp = minp_low_key(kNegInfKey16, ymax, thr, [](uint32_t kk) { return key16_value(kk); });
+    const uint32_t gm = (uint32_t)__builtin_popcountll(__ballot(in && yk >= ymp));
+    if (gm == 0u) {  // not reached: the maximum passes every non-NaN threshold
+      if (lane == 0u) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_EMPTY);
+      return true;
+    }
+    if (gm < G) {  // the cut ends above the K-th token's group: group gm - 1 is kept whole
+      last = gm - 1u;
+      last_keep = (uint32_t)__builtin_amdgcn_readlane((int)gcnt, (int)last);
+      cand_mass = at(incm, last);
+    }
+    if (minp_near(key16_value(ymp), M, thr) || (ymp > kNegInfKey16 && minp_near(key16_value(ymp - 1u), M, thr)))
+      flags |= LMRS_ROW_NEAR_BOUNDARY;
+  }
+  if (!(__builtin_isfinite(cand_mass) && cand_mass > 0.0)) {  // (strategies/mod.rs:39-43)
+    if (lane == 0u) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_DISTRIBUTION);
+    return true;
+  }
+  // inclusive mass of each group, the last one cut to its kept tokens
+  auto cum_of = [&](uint32_t lst, uint32_t lkeep) { return lane < lst ? incm : excl + (double)lkeep * w; };
+  double kept = cand_mass;
+  if (c.top_p < 1.0) {  // nucleus cut (top_p.rs:45-58) over the candidates
+    const double tp = c.top_p * cand_mass;
+    const uint64_t hit = __ballot(lane <= last && cum_of(last, last_keep) >= tp);
+    const uint32_t f = hit ? (uint32_t)__builtin_ctzll(hit) : last;
+    const double wf = at(w, f), ef = at(excl, f);
+    const uint32_t gmax = f == last ? last_keep : (uint32_t)__builtin_amdgcn_readlane((int)gcnt, (int)f);
+    double jj = ceil((tp - ef) * at(rw, f));
+    if (!(jj >= 1.0)) jj = 1.0;
+    if (jj > (double)gmax) jj = (double)gmax;
+    const uint32_t jp = (uint32_t)jj;
+    kept = ef + (double)jp * wf;
+    const double rc = 1.0 / cand_mass, accp = kept * rc, prev = (kept - wf) * rc;
+    double m = c.top_p - prev;
+    if (accp - c.top_p < m) m = accp - c.top_p;
+    if (m < 1e-6) flags |= LMRS_ROW_NEAR_BOUNDARY;
+    last = f;
+    last_keep = jp;
+  }
+  // the draw (softmax_choice, strategies/mod.rs:44-54)
+  const double target = c.u * kept;
+  const uint64_t hit = __ballot(lane <= last && cum_of(last, last_keep) >= target);
+  const uint32_t f = hit ? (uint32_t)__builtin_ctzll(hit) : last;  // fallback: the last kept token
+  const double wf = at(w, f), ef = at(excl, f);
+  const uint32_t gmax = f == last ? last_keep : (uint32_t)__builtin_amdgcn_readlane((int)gcnt, (int)f);
+  double jj = hit ? ceil((target - ef) * at(rw, f)) : (double)gmax;
+  if (!(jj >= 1.0)) jj = 1.0;
+  if (jj > (double)gmax) jj = (double)gmax;
+  const uint32_t jt = (uint32_t)jj;
+  const uint32_t gbf = (uint32_t)__builtin_amdgcn_readlane((int)gb, (int)f), ykf = y0 + gbf;
+  const uint32_t tok = jt == 1u ? uniform(binmin[gbf]) : stream_nth_index(sh, ykf, jt);
+  if (lane == 0u) {
+    // ln(w / kept) = (y - y0) - ln(kept), the difference exact in f32; ln(kept)
+    // from log2 of its mantissa in [0.5, 1) (within 1e-7) and its exponent
+    const float yv = key16_value(ykf);
+    int ek;
+    const double mk = frexp(kept, &ek);
+    const double lnk = ((double)__builtin_amdgcn_logf((float)mk) + (double)ek) * 0.6931471805599453;
+    const double rk = 1.0 / kept;
+    const double lo_c = (ef + (double)(jt - 1u) * wf) * rk, hi_c = lo_c + wf * rk;
+    double m = 1.0;
+    if (!(f == 0u && jt == 1u) && fabs(c.u - lo_c) < m) m = fabs(c.u - lo_c);
+    if (!(f == last && jt == gmax) && fabs(hi_c - c.u) < m) m = fabs(hi_c - c.u);
+    if (!hit) m = 0.0;
+    write_row(a, r, tok, (float)((double)(yv - key16_value(y0)) - lnk), yv,
+              flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+  }
+  return true;
+}
+
+// ---- the lean pass of greedy and small-k rows ----------------------------------------
+//
+// A row that keeps at most kSmallK tokens by top-k (greedy included), whose
+// penalties can only lower a history token's logit, is selected while it
+// streams in, with as few instructions per slot as possible (each one runs
+// on eight waves that share four SIMDs):
+//   * per slot, the chunk's maximum as signed 16-bit integers of the raw
+//     bf16 patterns -- the true maximum whenever it is not negative -- and
+//     the unsigned maximum, which exposes a negative NaN;
+//   * from slot kHashFrom the history ids go into an LDS hash (token ->
+//     multiplicity), one a slot, while the row streams in;
+//   * at slot kBoundAt (half the row; from slot kDeepAt every later slot is
+//     requested) a bound: each wave takes the ceil(K/8)-th largest of its threads'
+//     running maxima, and the row's bound za is the smallest of the eight.
+//     Every chunk whose maximum reaches za is recorded (raw words and index)
+//     in its wave's LDS segment, those of the slots already in registers at
+//     once, the later ones as they land;
+//   * after the last slot each wave turns its own records into candidates:
+//     elements with z >= za (a history token by its penalised z, which is
+//     never above its raw logit here), each listed as (y key, index) and
+//     counted in a histogram over y keys, and its index in the lowest index
+//     of its bin; one barrier, then stream_finish.
+// Nothing here has to be a proof: za stands for the values of real elements
+// only when they are not negative, and any number of history tokens may sit
+// among the maxima.  What matters is that every element with z >= za is
+// listed: if at least K are, the K largest by (y, index) are among them, and
+// stream_finish checks that count -- and that the K-th is not in the lowest
+// listed group when under temperature that group also holds keys below za.  A row that has fewer, a negative bound,
+// a NaN, or more records or candidates than a segment holds declines, and
+// the general pass takes it from the registers.
+
+// Signed maximum of the eight bf16 patterns of a chunk (as int16): the
+// largest value when any value is >= +0.0.  The words are copied out first:
+// a __builtin_bit_cast of an element of a vector reference (w[1]) is
+// compiled here as a cast of the vector's first element.
+__device__ __forceinline__ int32_t chunk_smax(const u32x4 &w) {
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3];
+  const i16x2 a = __builtin_elementwise_max(__builtin_bit_cast(i16x2, w0), __builtin_bit_cast(i16x2, w1));
+  const i16x2 b = __builtin_elementwise_max(__builtin_bit_cast(i16x2, w2), __builtin_bit_cast(i16x2, w3));
+  const i16x2 m = __builtin_elementwise_max(a, b);
+  return max((int32_t)m.x, (int32_t)m.y);
+}
+
+// Unsigned maxima of the bf16 patterns (two halves): a negative NaN is a
+// pattern above 0xFF80.
+__device__ __forceinline__ uint32_t chunk_umax(const u32x4 &w) {
+  return pk_max_u16(pk_max_u16(w[0], w[1]), pk_max_u16(w[2], w[3]));
+}
+
+__device__ __forceinline__ uint32_t lean_hash_slot(uint32_t t) { return (t * 2654435761u) >> (32 - kLHashBits); }
+
+// Adds one occurrence of history token t (t < V) to the hash.
+__device__ __forceinline__ void lean_hash_add(uint32_t *h, uint32_t t) {
+  const uint32_t key = t + 1u;
+  for (uint32_t s = lean_hash_slot(t);; s = (s + 1u) & (kLHashSlots - 1)) {  // ends: at most half full
+    const uint32_t old = atomicCAS(&h[s], 0u, key | (1u << 18));
+    if (old == 0u) return;
+    if ((old & 0x3FFFFu) == key) {
+      atomicAdd(&h[s], 1u << 18);
+      return;
+    }
+  }
+}
+
+// Multiplicity of token t in the history (0: not a history token).
+__device__ __forceinline__ uint32_t lean_hash_count(const uint32_t *h, uint32_t t) {
+  const uint32_t key = t + 1u;
+  for (uint32_t s = lean_hash_slot(t);; s = (s + 1u) & (kLHashSlots - 1)) {
+    const uint32_t v = h[s];
+    if (v == 0u) return 0u;
+    if ((v & 0x3FFFFu) == key) return v >> 18;
+  }
+}
+
+// Whether a row's penalties can only lower a history token's logit (then
+// z <= raw for every element): repetition >= 1, presence and frequency >= 0.
+__device__ __forceinline__ bool penalties_lower(const RowCfg &c) {
+  return (!c.rep_on || c.nf >= 1.0f) && (!c.pres_on || (c.presence >= 0.0f && c.frequency >= 0.0f));
+}
+
+// The lean pass of one row.  On entry slots 0 .. kPre - 1 and the history
+// ids are requested; returns true when the row is written, false (uniformly)
+// when the general pass must take it, with every slot waited for in kv (raw
+// patterns) and the history ids in hid.
+template <int NCH, int kPre>
+__device__ __forceinline__ bool lean_row(FastShared &sh, const lmrs_sample_args &a, int r, const RowCfg &c,
+                                         u32x4 (&kv)[NCH], uint32_t (&hid)[kHistPer], bool hist, const uint4 *src,
+                                         int nchunks) {
+  const int tid = threadIdx.x;
+  const uint32_t lane = (uint32_t)tid & 63u;
+  const int wave = tid >> 6;
+  const int64_t V = a.vocab;
+  constexpr int kEarly = NCH / 4;      // slots in flight ahead of the one being processed
+  constexpr int kBoundAt = NCH / 2;    // the bound is taken before this slot is waited for
+  constexpr int kDeepAt = NCH / 2;     // from this slot on, every slot of the row is requested
+  constexpr int kHashFrom = kPre + 1;  // from this slot, kHashPer history ids a slot enter the hash
+  constexpr int kHashPer = (kHistPer + (NCH - kHashFrom) - 1) / (NCH - kHashFrom);
+  static_assert(kPre <= kEarly && kBoundAt > kPre && kDeepAt <= kBoundAt, "lean schedule");
+  // the last slot requested before slot s is waited for: kEarly ahead, and
+  // every slot of the row from kDeepAt on
+  constexpr auto last_issued = [](int s) constexpr {
+    if (s < 0) return kEarly - 1;
+    const int l = s >= kDeepAt ? NCH - 1 : s + kEarly;
+    return l < NCH - 1 ? l : NCH - 1;
+  };
+  auto issue_slot = [&](int s) {
+    const int ch = s * kFT + tid;
+    return issue_load_b128(ch < nchunks ? src + ch : &kNegInfChunk);  // lanes past the end load -inf
+  };
+#pragma unroll
+  for (int s = kPre; s < kEarly; ++s) kv[s] = issue_slot(s);
+  uint32_t *hash = sh.u32(kLOffHash);
+  {  // cleared before the bound's barrier; the histogram and the flag are used after the last slot
+    if (hist) {
+      uint4 *h4 = (uint4 *)hash;
+#pragma unroll
+      for (int i = 0; i < kLHashSlots / 4 / kFT; ++i) h4[i * kFT + tid] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    static_assert(kCandBins == kFT, "one candidate bin per thread");
+    sh.u32(kOffCandHist)[tid] = 0u;
+    sh.u32(kLOffBinMin)[tid] = 0xFFFFFFFFu;
+    if (tid < 2) sh.counters()[kCtrLeanBad + tid] = 0u;
+  }
+  if (hist) __syncthreads();  // the hash is clear (while the first slots are in flight)
+  const uint32_t K = (uint32_t)c.top_k;
+  const uint32_t kw = (K + kFW - 1u) / kFW;  // each wave's share of the bound (<= 8)
+  bool live = true, tie_below = false;        // (uniform)
+  int32_t tv = -0x8000, cmr[kBoundAt], zas = 0x7FFFFFFF;
+  uint32_t nacc = 0u, za = 0xFFFFu, y0 = 0u, wrec = 0u;
+  uint4 *rec_raw = (uint4 *)sh.u32(kLOffRecRaw) + wave * kRecSeg;
+  uint32_t *rec_ch = sh.u32(kLOffRecCh) + wave * kRecSeg;
+  auto record = [&](const u32x4 &w, uint32_t ch, bool hit) {  // (all lanes of the wave)
+    const uint64_t m = __ballot(hit);
+    if (m) {
+      const uint32_t pos = wrec + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (hit && pos < (uint32_t)kRecSeg) {
+        rec_raw[pos] = make_uint4(w[0], w[1], w[2], w[3]);
+        rec_ch[pos] = ch;
+      }
+      wrec += (uint32_t)__builtin_popcountll(m);
+    }
+  };
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    constexpr int last = last_issued(s), prev = last_issued(s - 1);
+    static_for<prev + 1, last + 1>([&](auto T) { kv[decltype(T)::value] = issue_slot(decltype(T)::value); });
+    // loads issued after slot s's: later slots, and the history ids for the first kPre slots
+    constexpr int younger = last - s + (s < kPre ? kHistPer : 0);
+    if constexpr (s == kBoundAt) {
+      // each wave's kw-th largest running maximum, then the smallest over the waves
+      int32_t v = tv, lw = -0x8000;
+      for (uint32_t i = 0u; i < kw; ++i) {
+        lw = wave_max(v);
+        const uint64_t h = __ballot(v == lw);
+        if (lane == (uint32_t)__builtin_ctzll(h)) v = -0x8000;  // one copy leaves
+      }
+      if (lane == 0u) sh.lean_l[wave] = lw;
+      __syncthreads();
+      int32_t L = sh.lean_l[0];
+#pragma unroll
+      for (int w = 1; w < kFW; ++w) L = min(L, sh.lean_l[w]);
+      L = uniform(L);
+      live = L >= 0;  // (a negative bound: the signed maxima do not stand for the values)
+      if (live) {
+        za = (uint32_t)L | 0x8000u;
+        zas = L;
+        y0 = temp_key16(za, c);
+        // y0's group may hold elements below za, which are not listed
+        tie_below = za > 0x8000u && temp_key16(za - 1u, c) == y0;
+        // every candidate bin's weight exp(y - y0), while the rest of the row
+        // streams in (keys at most 510 apart are at most four binades apart:
+        // their f32 difference is exact); a weight that overflows is a
+        // reason to decline
+        if (tid < kCandBins - 1) {
+          const double wt = exp((double)(key16_value(min(y0 + (uint32_t)tid, 0xFFFFu)) - key16_value(y0)));
+          ((double *)sh.u32(kLOffWbin))[tid] = wt;
+        }
+        static_for<0, kBoundAt>([&](auto T) {
+          constexpr int t = decltype(T)::value;
+          record(kv[t], (uint32_t)(t * kFT + tid), cmr[t] >= zas);
+        });
+      }
+    }
+    wait_loads<younger>(kv[s]);
+    if constexpr (s == kPre) {  // the history ids were requested before this slot
+#pragma unroll
+      for (int q = 0; q < kHistPer; ++q) wait_loads<younger>(hid[q]);
+    }
+    if constexpr (s >= kHashFrom) {
+      // kHashPer history ids a slot into the hash, while the row streams in
+      // (complete at the barrier after the last slot)
+#pragma unroll
+      for (int q = (s - kHashFrom) * kHashPer; q < (s - kHashFrom + 1) * kHashPer && q < kHistPer; ++q)
+        if (hist && history_live(q, hid[q], c.h_len, V)) lean_hash_add(hash, hid[q]);
+    }
+    const int32_t cm = chunk_smax(kv[s]);
+    nacc = pk_max_u16(nacc, chunk_umax(kv[s]));
+    if constexpr (s < kBoundAt) {
+      tv = max(tv, cm);
+      cmr[s] = cm;
+    } else {
+      if (live) record(kv[s], (uint32_t)(s * kFT + tid), cm >= zas);
+    }
+  });
+  if (!live) return false;
+  // a negative NaN anywhere (positive NaNs are recorded, as they pass za)
+  if (max(nacc & 0xFFFFu, nacc >> 16) >= 0xFF81u) atomicOr(&sh.counters()[kCtrLeanBad], 1u);
+  // the hash is complete once every wave has passed this barrier
+  __syncthreads();
+  // every wave lists the candidates of its records
+  uint64_t *seg = (uint64_t *)sh.u32(kOffCand) + wave * kCandSeg;
+  uint32_t *chist = sh.u32(kOffCandHist);
+  uint32_t wn = 0u, ymx = 0u, nan = 0u;
+  if (lane < wrec && lane < (uint32_t)kRecSeg) {
+    const uint4 raw = rec_raw[lane];
+    const uint32_t ch = rec_ch[lane];
+    const uint4 kw4 = make_uint4(key_pair(raw.x), key_pair(raw.y), key_pair(raw.z), key_pair(raw.w));
+    for (uint32_t e8 = chunk_ge(kw4, za); e8; e8 &= e8 - 1u) {
+      const uint32_t e = (uint32_t)__builtin_ctz(e8), idx = ch * 8u + e;
+      uint32_t zk = chunk_key(kw4, e);
+      if (hist) {
+        const uint32_t cnt = lean_hash_count(hash, idx);
+        if (cnt) zk = bits_key16(penalise_member(key16_bits(zk), cnt, c));
+      }
+      nan |= is_nan_key16(zk) ? 1u : 0u;
+      // listing positions: every lane in the loop has taken the same
+      // iterations, so they all hold the same wn
+      const bool put = zk >= za;
+      const uint64_t m = __ballot(put);
+      if (put) {
+        const uint32_t yk = temp_key16(zk, c);
+        ymx = max(ymx, yk);
+        atomicAdd(&chist[min(yk - y0, (uint32_t)kCandBins - 1u)], 1u);
+        atomicMin(&sh.u32(kLOffBinMin)[min(yk - y0, (uint32_t)kCandBins - 1u)], idx);
+        const uint32_t pos = wn + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        if (pos < (uint32_t)kCandSeg) seg[pos] = ((uint64_t)yk << 32) | idx;
+      }
+      wn += (uint32_t)__builtin_popcountll(m);
+    }
+  }
+  wn = wave_max(wn);
+  ymx = wave_max(ymx);
+  const bool decline = __ballot(nan != 0u) || wrec > (uint32_t)kRecSeg || wn > (uint32_t)kCandSeg;
+  if (lane == 0u) {
+    sh.cand_n[wave] = wn;
+    // a NaN, or dropped records or candidates: decline
+    if (decline) atomicOr(&sh.counters()[kCtrLeanBad], 1u);
+    atomicMax(&sh.counters()[kCtrLeanYmax], ymx);
+  }
+  __syncthreads();
+  return stream_finish(sh, a, r, c, K, y0, tie_below);
+}
+
 // ---- one row ----------------------------------------------------------------------
 
 // Returns false (uniformly) when the row must go to the generic engine,
@@ -1142,6 +1623,18 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
   uint32_t hid[kHistPer];
   issue_history_ids(hid, a, c, hist, rowp);
+  const bool k_on = c.top_k > 0 && c.top_k < V;
+  // Greedy and small-k rows whose penalties only lower logits take the lean
+  // pass; one that declines is read again by the general pass, in the same
+  // order of requests.
+  const bool lean = c.status == LMRS_ROW_OK && (c.greedy || (k_on && c.top_k <= kSmallK)) && penalties_lower(c);
+  if (lean) {
+    if (lean_row<NCH, kPre>(sh, a, r, c, kv, hid, hist, src, nchunks)) return true;
+    __syncthreads();  // the lean pass's LDS views are dead
+#pragma unroll
+    for (int s = 0; s < kPre; ++s) kv[s] = issue_slot(s);
+    issue_history_ids(hid, a, c, hist, rowp);
+  }
 #pragma unroll
   for (int s = kPre; s < kEarly; ++s) kv[s] = issue_slot(s);
   clear_tables(sh, hist, nwords);
@@ -1236,7 +1729,6 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   // NaNs, which the key map does not model.
   if (bad || tvhi == 0u) return false;
   tvlo = ~tvlo;  // the smallest nonzero thread value
-  const bool k_on = c.top_k > 0 && c.top_k < V;
   const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
   const uint4 *src2 = fresh(src);  // the re-reads
   SelState &ss = sh.ss();
