@@ -136,7 +136,9 @@ int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream);
  * LogitsProcessor::process (crates/sampling/src/logits/processor.rs:21-24)
  * for the three reference processors, batched.  Uses args' logits, dtype,
  * batch, vocab, row_stride, history and the three penalty / temperature
- * arrays; ignores the rest. */
+ * arrays (status[r], when given, reports a penalty, temperature or history
+ * that fails its check, and such a row is copied unchanged); top_k, top_p,
+ * min_p, uniforms and the other outputs are neither read nor checked. */
 int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, void *stream);
 
 /* Device workspace, in bytes, that lmrs_sample_fwd needs for a call of this

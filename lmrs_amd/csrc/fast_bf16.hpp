@@ -278,6 +278,7 @@ constexpr int kOffMatch = kOffGroups + 64 * 8;
 constexpr int kCtrLeanBad = 6;           // counters() words of the lean pass: a reason to decline,
 constexpr int kCtrLeanYmax = 7;          // and the largest listed y key
 constexpr int kLOffWbin = 64 * 1024;     // lean pass: exp(y - y0) of each candidate bin (f64)
+constexpr int kFinishBins = 256;         // the bins stream_finish scans below the largest key
 static_assert(kLOffHash + kLHashSlots * 4 <= kLOffRecRaw && kLOffBinMin + kCandBins * 4 <= kOffCand, "lean views");
 static_assert(kOffMatch + kFW * kCandSeg * 4 <= kOffWhist, "candidate views");
 static_assert(LMRS_MAX_HISTORY * 2 <= kLHashSlots && kFastMaxVocab < (1 << 18) && LMRS_MAX_HISTORY < (1 << 14),
@@ -1197,6 +1198,7 @@ __device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_
   const uint32_t *hb = sh.u32(kOffCandHist);
   uint32_t base = 0u, G = 0u, keep_k = 0u, packed = 0u;
   bool found = false;
+  static_assert(kFinishBins == 4 * 64, "four rounds of 64 bins");
   for (int e = 0; e < 4 && !found; ++e) {
     const int bl = (int)bmax - (int)lane - 64 * e;
     const uint32_t cnt = bl >= 0 ? hb[bl] : 0u;
@@ -1473,13 +1475,17 @@ __device__ __forceinline__ bool lean_row(FastShared &sh, const lmrs_sample_args 
     // loads issued after slot s's: later slots, and the history ids for the first kPre slots
     constexpr int younger = last - s + (s < kPre ? kHistPer : 0);
     if constexpr (s == kBoundAt) {
-      // each wave's kw-th largest running maximum, then the smallest over the waves
-      int32_t v = tv, lw = -0x8000;
-      for (uint32_t i = 0u; i < kw; ++i) {
-        lw = wave_max(v);
-        const uint64_t h = __ballot(v == lw);
-        if (lane == (uint32_t)__builtin_ctzll(h)) v = -0x8000;  // one copy leaves
+      // each wave's kw-th largest running maximum (the largest t with at
+      // least kw values >= t, one bit at a time on a uniform t), then the
+      // smallest over the waves
+      const uint32_t v = (uint32_t)(tv + 0x8000);  // order-preserving in [0, 0xFFFF]
+      uint32_t t = 0u;
+#pragma unroll
+      for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t tt = t | (1u << bit);
+        if ((uint32_t)__builtin_popcountll(__ballot(v >= tt)) >= kw) t = tt;
       }
+      const int32_t lw = (int32_t)t - 0x8000;
       if (lane == 0u) sh.lean_l[wave] = lw;
       __syncthreads();
       int32_t L = sh.lean_l[0];
@@ -1507,17 +1513,18 @@ __device__ __forceinline__ bool lean_row(FastShared &sh, const lmrs_sample_args 
         });
       }
     }
+    if constexpr (s >= kHashFrom) {
+      // kHashPer history ids a slot into the hash (complete at the barrier
+      // after the last slot), before the slot's wait, which hides the
+      // atomics' round trips
+#pragma unroll
+      for (int q = (s - kHashFrom) * kHashPer; q < (s - kHashFrom + 1) * kHashPer && q < kHistPer; ++q)
+        if (hist && history_live(q, hid[q], c.h_len, V)) lean_hash_add(hash, hid[q]);
+    }
     wait_loads<younger>(kv[s]);
     if constexpr (s == kPre) {  // the history ids were requested before this slot
 #pragma unroll
       for (int q = 0; q < kHistPer; ++q) wait_loads<younger>(hid[q]);
-    }
-    if constexpr (s >= kHashFrom) {
-      // kHashPer history ids a slot into the hash, while the row streams in
-      // (complete at the barrier after the last slot)
-#pragma unroll
-      for (int q = (s - kHashFrom) * kHashPer; q < (s - kHashFrom + 1) * kHashPer && q < kHistPer; ++q)
-        if (hist && history_live(q, hid[q], c.h_len, V)) lean_hash_add(hash, hid[q]);
     }
     const int32_t cm = chunk_smax(kv[s]);
     nacc = pk_max_u16(nacc, chunk_umax(kv[s]));
@@ -1627,13 +1634,17 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   // Greedy and small-k rows whose penalties only lower logits take the lean
   // pass; one that declines is read again by the general pass, in the same
   // order of requests.
-  const bool lean = c.status == LMRS_ROW_OK && (c.greedy || (k_on && c.top_k <= kSmallK)) && penalties_lower(c);
-  if (lean) {
-    if (lean_row<NCH, kPre>(sh, a, r, c, kv, hid, hist, src, nchunks)) return true;
-    __syncthreads();  // the lean pass's LDS views are dead
+  // (not in the widest instantiation: its registers would spill)
+  const bool lean = NCH <= 32 && c.status == LMRS_ROW_OK && (c.greedy || (k_on && c.top_k <= kSmallK)) &&
+                    penalties_lower(c);
+  if constexpr (NCH <= 32) {
+    if (lean) {
+      if (lean_row<NCH, kPre>(sh, a, r, c, kv, hid, hist, src, nchunks)) return true;
+      __syncthreads();  // the lean pass's LDS views are dead
 #pragma unroll
-    for (int s = 0; s < kPre; ++s) kv[s] = issue_slot(s);
-    issue_history_ids(hid, a, c, hist, rowp);
+      for (int s = 0; s < kPre; ++s) kv[s] = issue_slot(s);
+      issue_history_ids(hid, a, c, hist, rowp);
+    }
   }
 #pragma unroll
   for (int s = kPre; s < kEarly; ++s) kv[s] = issue_slot(s);

@@ -651,7 +651,7 @@ __global__ void __launch_bounds__(kThreads) process_kernel(lmrs_sample_args a, v
   __shared__ HistoryTables ht;
   __shared__ RowCfg cfg;
   const int r = blockIdx.x;
-  if (threadIdx.x == 0) cfg = load_row_cfg(a, r, DT);
+  if (threadIdx.x == 0) cfg = load_row_cfg(a, r, DT, false);
   __syncthreads();
   RowCfg c = cfg;
   const int64_t V = a.vocab;

@@ -87,17 +87,19 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
 // (temperature.rs:43-50), TopP::new (top_p.rs:26-31), MinP::new
 // (min_p.rs:27-29, a negative value switching the cut off); top_k below
 // LMRS_GREEDY invalid.  Greedy rows carry top_k = 1 with `greedy` set.
-__device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype) {
+// With strategy == false (the processor chain alone) the top-k, top-p and
+// min-p fields are neither read nor checked.
+__device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype, bool strategy = true) {
   RowCfg c;
   c.status = LMRS_ROW_OK;
   float rep = a.repetition_penalty ? a.repetition_penalty[r] : 1.0f;
   float pres = a.presence_penalty ? a.presence_penalty[r] : 0.0f;
   float freq = a.frequency_penalty ? a.frequency_penalty[r] : 0.0f;
   double t = a.temperature ? a.temperature[r] : 1.0;
-  int64_t k = a.top_k ? (int64_t)a.top_k[r] : 0;
-  double p = a.top_p ? a.top_p[r] : 1.0;
-  double mp = a.min_p ? a.min_p[r] : -1.0;
-  c.u = a.uniforms ? a.uniforms[r] : 0.0;
+  int64_t k = strategy && a.top_k ? (int64_t)a.top_k[r] : 0;
+  double p = strategy && a.top_p ? a.top_p[r] : 1.0;
+  double mp = strategy && a.min_p ? a.min_p[r] : -1.0;
+  c.u = strategy && a.uniforms ? a.uniforms[r] : 0.0;
   if (!(__builtin_isfinite(rep) && rep > 0.0f) || !__builtin_isfinite(pres) ||
       !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < LMRS_GREEDY ||
       !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0) || __builtin_isnan(mp) || mp > 1.0)

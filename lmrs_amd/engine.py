@@ -102,6 +102,22 @@ class SequenceState:
         self.rng = max(int(self.seed), 1)
 
 
+_ROW_MESSAGES = {S.ROW_EMPTY: "cannot sample from empty logits",
+                 S.ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
+                 S.ROW_PARAM: "invalid sampling parameter", S.ROW_HISTORY: "history too long"}
+
+
+class BatchSamplingError(S.SamplingError):
+    """Some sequences of a decode step failed (SamplingError::Invalid per
+    sequence); `errors` maps their indices to the reference's messages and
+    `outputs` holds the step's outputs of the sequences that committed."""
+
+    def __init__(self, errors: dict, outputs: list):
+        super().__init__("; ".join(f"sequence {i}: {m}" for i, m in sorted(errors.items())))
+        self.errors = errors
+        self.outputs = outputs
+
+
 class DecodeBatch:
     """Samples the next token of every live sequence with one launch."""
 
@@ -142,11 +158,20 @@ class DecodeBatch:
         lg = res["logits"].cpu().numpy()
         st = res["status"].cpu().numpy() & 0xFF
         out: List[Optional[S.SampleOutput]] = [None] * len(self.sequences)
+        # Every row's status is known before any state changes.  A failing
+        # sequence keeps its generator as it was (the reference draws only
+        # after validation, strategies/mod.rs:39-44) and gets no token; the
+        # others commit, as each sequence's own generate loop would
+        # (generation.rs:327-346), and the failures are raised together.
+        errors = {}
         for j, i in enumerate(live):
-            s = self.sequences[i]
             if st[j] != S.ROW_OK:
-                s.rng = saved[j]  # the reference draws only after validation
-                raise S.SamplingError(f"sequence {i}: row status {int(st[j])}")
+                self.sequences[i].rng = saved[j]
+                errors[i] = _ROW_MESSAGES.get(int(st[j]), f"row status {int(st[j])}")
+        for j, i in enumerate(live):
+            if i in errors:
+                continue
+            s = self.sequences[i]
             o = S.SampleOutput(int(tok[j]), float(lp[j]), float(lg[j]))
             out[i] = o
             if s.eos_token is not None and o.token_id == s.eos_token:
@@ -155,6 +180,8 @@ class DecodeBatch:
                 s.generated.append(o.token_id)
                 if len(s.generated) >= s.config.max_tokens:
                     s.finished = True
+        if errors:
+            raise BatchSamplingError(errors, out)
         return out
 
 
@@ -210,7 +237,7 @@ class GenerateParams:
     @classmethod
     def from_request(cls, req: dict) -> "GenerateParams":
         """From a completion or chat request's optional fields (openai.rs:160-182)."""
-        return cls(req.get("max_tokens") or 128,
+        return cls(128 if req.get("max_tokens") is None else req["max_tokens"],  # unwrap_or(128): 0 stays 0
                    1.0 if req.get("temperature") is None else req["temperature"],
                    1.0 if req.get("top_p") is None else req["top_p"],
                    req.get("top_k"), tuple(req.get("stop") or ()))

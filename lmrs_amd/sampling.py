@@ -100,6 +100,21 @@ def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def _on_stream(stream, tensors) -> None:
+    """Orders a launch on `stream` after the current stream's work (where the
+    argument tensors were allocated and filled) and marks the tensors as used
+    on `stream`, so that the caching allocator does not hand their memory to
+    another allocation before `stream` has read them."""
+    torch = _torch()
+    cur = torch.cuda.current_stream(stream.device)
+    if stream == cur:
+        return
+    stream.wait_stream(cur)
+    for t in tensors:
+        if t is not None:
+            t.record_stream(stream)
+
+
 def _dev_array(values, dtype, device):
     torch = _torch()
     if values is None:
@@ -194,6 +209,7 @@ def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty
                        frequency_penalty=frequency_penalty, temperature=temperature, top_k=top_k,
                        top_p=top_p, uniforms=uniforms, min_p=min_p, out=out)
     s = stream if stream is not None else torch.cuda.current_stream(logits.device)
+    _on_stream(s, list(pb._keep) + [v for k, v in pb.out.items() if k != "_keep"])
     pb.launch(s)
     out = pb.out
     # keep argument tensors alive until the stream has consumed them
@@ -221,6 +237,7 @@ def process_logits(logits, *, hist_offsets=None, hist_ids=None, repetition_penal
                       presence_penalty=_ptr(pp), frequency_penalty=_ptr(fp), temperature=_ptr(tt),
                       status=_ptr(status))
     s = stream if stream is not None else torch.cuda.current_stream(dev)
+    _on_stream(s, [logits, rp, pp, fp, tt, hist_offsets, hist_ids, status, out])
     rc = lib().lmrs_process_logits_fwd(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()),
                                        ctypes.c_void_p(s.cuda_stream))
     if rc != LMRS_OK:

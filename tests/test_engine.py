@@ -145,6 +145,8 @@ def test_generate_params_wire_format():
     assert E.sampler_for(g).temperature == 0.699999988079071
     r = E.GenerateParams.from_request({"max_tokens": None, "temperature": 0.5, "stop": ["\n"]})
     assert (r.max_tokens, r.temperature, r.top_p, r.top_k, r.stop) == (128, 0.5, 1.0, None, ("\n",))
+    # unwrap_or(128) keeps an explicit 0 (openai.rs:160-170)
+    assert E.GenerateParams.from_request({"max_tokens": 0}).max_tokens == 0
     with pytest.raises(ValueError):
         E.GenerateParams(temperature=0.0).to_generation_config()
 
@@ -212,3 +214,26 @@ def test_run_batch_matches_successive_sample_calls():
         for j in range(B):
             b.sample(y[j, -1])
     assert a.rng == b.rng
+
+
+@pytest.mark.gpu
+def test_decode_step_failure_commits_the_other_sequences():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    S.lib()
+    V = 4096
+    seqs = [E.SequenceState(E.GenerationConfig(8, 1.0, 1.0, 20), seed=7 + i) for i in range(3)]
+    batch = E.DecodeBatch(seqs)
+    x = torch.randn(3, V).to(torch.bfloat16)
+    x[1, 5] = float("nan")  # TopK(20) over a NaN row: invalid distribution (strategies/mod.rs:39-43)
+    rngs = [s.rng for s in seqs]
+    with pytest.raises(E.BatchSamplingError) as ei:
+        batch.step(x.cuda())
+    err = ei.value
+    assert set(err.errors) == {1} and "invalid probability distribution" in err.errors[1]
+    assert seqs[1].rng == rngs[1] and seqs[1].generated == []          # no draw, no token
+    for i in (0, 2):                                                  # the others committed
+        assert seqs[i].rng == S.next_unit(rngs[i])[1]
+        assert len(seqs[i].generated) == 1 and err.outputs[i].token_id == seqs[i].generated[0]
+    assert err.outputs[1] is None

@@ -116,6 +116,47 @@ def test_processors_exhaustive_bf16():
         assert len(bad) == 0, (rows[r], bad[:8], got[r][bad[:8]], want[bad[:8]])
 
 
+def test_process_logits_ignores_the_strategy_fields():
+    # lmrs_process_logits_fwd is LogitsProcessor::process: an invalid top_p,
+    # top_k or min_p in the argument block is neither read nor reported
+    import ctypes
+
+    from lmrs_amd import sampling as S
+
+    B, V = 4, 1000
+    x = torch.randn(B, V).to(torch.bfloat16).cuda()
+    tt = torch.full((B,), 0.7, dtype=torch.float64, device="cuda")
+    bad_p = torch.full((B,), 1.5, dtype=torch.float64, device="cuda")
+    bad_k = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+    status = torch.full((B,), 99, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(x)
+    args = S.SampleArgs(logits=x.data_ptr(), dtype=S.DTYPE_BF16, batch=B, vocab=V, row_stride=V,
+                        temperature=tt.data_ptr(), top_p=bad_p.data_ptr(), top_k=bad_k.data_ptr(),
+                        status=status.data_ptr())
+    s = torch.cuda.current_stream()
+    assert S.lib().lmrs_process_logits_fwd(ctypes.byref(args), ctypes.c_void_p(out.data_ptr()),
+                                           ctypes.c_void_p(s.cuda_stream)) == S.LMRS_OK
+    torch.cuda.synchronize()
+    assert status.cpu().tolist() == [S.ROW_OK] * B
+    want, _ = S.process_logits(x, temperature=[0.7] * B)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
+def test_sampling_on_a_side_stream_waits_for_its_arguments():
+    from lmrs_amd import sampling as S
+
+    W = _wl()
+    w = W.c1(batch=4)
+    logits = torch.from_numpy(w.logits).cuda()
+    side = torch.cuda.Stream()
+    ref = run_oracle(w)
+    for _ in range(3):  # arguments built on the current stream, launched on the side stream
+        res = S.sample_batch(logits, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p,
+                             uniforms=w.uniforms, stream=side)
+        side.synchronize()
+        assert np.array_equal(res["token_ids"].cpu().numpy().view(np.uint32), ref["token_id"])
+
+
 def test_processors_f32():
     import oracle as O
 
