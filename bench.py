@@ -70,33 +70,46 @@ def read_traffic(name: str):
 
 def cpu_baseline(w, gpu_out, seconds: float):
     """Times the oracle (the C restatement of the reference's CPU sampler) on
-    the workload's rows for about `seconds` of wall time, and compares its
-    tokens with the GPU's."""
+    the workload's rows, and compares its tokens with the GPU's.  Two legs of
+    about `seconds` of wall time each: every available core with one row per
+    thread at a time, and one thread with the rows in order, as the
+    reference's worker samples a batch (crates/engine/src/worker/worker.rs:
+    137-157).  The first is `cpu_baseline`; the second is reported beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from helpers import compare, run_oracle
 
+    host_cores = os.cpu_count() or 1
     try:
-        cores = len(os.sched_getaffinity(0))
+        affinity = len(os.sched_getaffinity(0))
     except AttributeError:
-        cores = os.cpu_count() or 1
-    threads = max(1, min(16, cores))
-    # one pass over the batch, repeated until about `seconds` of wall time
-    t0 = time.perf_counter()
-    ref = run_oracle(w, threads=threads)
-    passes, dt = 1, time.perf_counter() - t0
-    while dt < seconds:
-        run_oracle(w, threads=threads)
-        passes += 1
-        dt = time.perf_counter() - t0
+        affinity = host_cores
+    # the GPU box grants 16 cores to a one-GPU job whatever the host has
+    threads = max(1, min(16, affinity))
+
+    def timed(nthreads, limit):
+        t0 = time.perf_counter()
+        ref = run_oracle(w, threads=nthreads)
+        passes, dt = 1, time.perf_counter() - t0
+        while dt < limit:
+            run_oracle(w, threads=nthreads)
+            passes += 1
+            dt = time.perf_counter() - t0
+        return ref, passes, dt
+
+    ref, passes, dt = timed(threads, seconds)
+    _, passes1, dt1 = timed(1, seconds)
     n = w.batch
     gpu = {k: v[:n] for k, v in gpu_out.items()}
     rep = compare(gpu, ref)
     base = {"value": passes * n / dt, "unit": "rows/s", "cores": threads, "kind": "port",
             "sample": f"{passes} passes over all {n} rows of {w.name} ({dt:.1f} s, {threads} threads, "
-                      f"oracle/lmrs_oracle.c sample_batch, one row per thread at a time)"}
+                      f"oracle/lmrs_oracle.c sample_batch, one row per thread at a time)",
+            "host_cores": host_cores, "affinity_cores": affinity,
+            "one_thread": {"value": passes1 * n / dt1, "unit": "rows/s", "cores": 1,
+                           "sample": f"{passes1} passes over all {n} rows in order on one thread ({dt1:.1f} s)"}}
     parity = {k: rep[k] for k in ("rows", "status_mismatch", "token_mismatch", "boundary_rows",
-                                  "boundary_mismatch", "logit_mismatch", "max_prob_rel_err")}
+                                  "boundary_mismatch", "logit_mismatch", "max_prob_rel_err", "gpu_flagged")}
     return base, parity
 
 
@@ -222,20 +235,32 @@ def main() -> int:
 
     stream = torch.cuda.Stream(device=dev)
     torch.cuda.synchronize()
+    # The timed steps run back to back on one stream; an event every
+    # GROUP steps gives the spread (median, p10, p90 of the group means)
+    # without a gap between steps.
+    GROUP = 10
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
             batches[i % nrot].launch(stream)
         stream.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        events = [torch.cuda.Event(enable_timing=True)]
         torch.cuda.synchronize()
-        start.record(stream)
+        events[0].record(stream)
         for i in range(args.steps):
             batches[i % nrot].launch(stream)
-        end.record(stream)
-        end.synchronize()
+            if (i + 1) % GROUP == 0 or i + 1 == args.steps:
+                events.append(torch.cuda.Event(enable_timing=True))
+                events[-1].record(stream)
+        events[-1].synchronize()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / max(1, args.steps)
-    log(f"bench: {args.steps} steps, {ms * 1e3:.1f} us/step")
+    ms = events[0].elapsed_time(events[-1]) / max(1, args.steps)
+    sizes = [GROUP] * (args.steps // GROUP) + ([args.steps % GROUP] if args.steps % GROUP else [])
+    group_us = sorted(1e3 * events[j].elapsed_time(events[j + 1]) / sizes[j] for j in range(len(sizes)))
+    pct = lambda q: group_us[min(len(group_us) - 1, int(q * (len(group_us) - 1) + 0.5))]  # noqa: E731
+    spread = {"median": pct(0.5), "p10": pct(0.1), "p90": pct(0.9), "unit": "us/step",
+              "over": f"{len(sizes)} groups of up to {GROUP} back-to-back steps"}
+    log(f"bench: {args.steps} steps, {ms * 1e3:.1f} us/step (median {spread['median']:.1f}, "
+        f"p10 {spread['p10']:.1f}, p90 {spread['p90']:.1f})")
     ceiling = stream_ceiling(bufs, args.steps, args.warmup, dev)
 
     # outputs of the last step (every rotation holds the same logits)
@@ -257,6 +282,7 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": ms,
         "us_per_step": ms * 1e3,
+        "us_per_step_spread": spread,
         "hbm_peak_pct": 100.0 * achieved / HBM_PEAK_GBS,
         "higher_is_better": True,
         "scaling": "weak",
