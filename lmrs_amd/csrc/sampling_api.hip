@@ -3,6 +3,7 @@
 // Host-side argument checks, then one launch of one workgroup per row on the
 // caller's stream.  Nothing here allocates device memory.
 #include "lmrs_sampling.h"
+#include "f32_dist.hpp"
 #include "fast_bf16.hpp"
 #include "generic_engine.hpp"
 
@@ -51,7 +52,7 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
   } else if (args->dtype == LMRS_DTYPE_BF16)
     lmrs::generic_sample_kernel<LMRS_DTYPE_BF16><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
   else
-    lmrs::generic_sample_kernel<LMRS_DTYPE_F32><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
+    lmrs::f32_sample_kernel<<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
   return hipGetLastError() == hipSuccess ? LMRS_OK : LMRS_ERR_LAUNCH;
 }
 

@@ -586,6 +586,57 @@ def test_randomized_rows_every_path():
         assert_parity(rep, f"randomized-{V}")
 
 
+def test_randomized_f32_rows_every_path():
+    """f32 rows of the two-pass kernel: the distributions its bins and
+    sub-buckets branch on (normal, heavy-tailed, flat, spiked, bf16-valued ties,
+    masked with -1e9 and -inf, ascending rows whose sample misjudges the
+    scale, all equal), with top-k partial bins, min-p partial bins, top-p,
+    temperature and histories, against the oracle."""
+    W = _wl()
+    rng = np.random.default_rng(4242)
+    for V, B in ((32000, 128), (256000, 48)):
+        rows, ks, ps, mps, ts, hists = [], [], [], [], [], []
+        for _ in range(B):
+            kind = rng.integers(9)
+            if kind == 0:
+                x = rng.normal(0, rng.uniform(0.02, 4.0), V)
+            elif kind == 1:
+                x = rng.standard_t(rng.uniform(1.5, 5.0), V) * rng.uniform(0.5, 3.0)
+            elif kind == 2:
+                x = rng.uniform(-1, 1, V) * 0.01
+            elif kind == 3:
+                x = rng.normal(0, 1, V)
+                x[rng.choice(V, rng.integers(1, 20), replace=False)] += rng.uniform(5, 30)
+            elif kind == 4:
+                x = W.bf16_bits_to_f32(W.f32_to_bf16_bits(rng.normal(0, 0.05, V).astype(np.float32)))
+            elif kind == 5:
+                x = rng.normal(0, 2, V)
+                x[rng.random(V) < 0.6] = -1e9
+                x[rng.random(V) < 0.1] = -np.inf
+            elif kind == 6:
+                x = np.sort(rng.normal(0, 2, V))          # the sample sees only the lowest values
+            elif kind == 7:
+                x = np.full(V, 0.25)
+            else:
+                x = rng.gumbel(0, 2.0, V)
+            rows.append(np.asarray(x, np.float32))
+            ks.append(int(rng.choice([0, 0, 0, -1, 1, 2, 10, 50, 1000, 5000, V + 3])))
+            ps.append(float(rng.choice([1.0, 0.99, 0.9, rng.uniform(0.05, 1.0), 0.999999])))
+            mps.append(float(rng.choice([-1.0, -1.0, -1.0, 0.0, rng.uniform(0, 0.5), 10 ** rng.uniform(-12, -1)])))
+            ts.append(float(rng.choice([1.0, 1.0, rng.uniform(0.3, 2.5)])))
+            hists.append(list(rng.integers(0, V, int(rng.choice([0, 0, 50, 512])))))
+        B = len(rows)
+        us = rng.random(B)
+        us[:4] = [0.0, 1 - 2.0 ** -52, 0.5, 1e-300]
+        w = _mk(np.stack(rows), k=np.array(ks, np.int32), p=np.array(ps), mp=np.array(mps), t=np.array(ts),
+                rep=rng.uniform(0.8, 1.5, B).astype(np.float32), pres=rng.uniform(-0.5, 1.0, B).astype(np.float32),
+                freq=rng.uniform(0, 0.5, B).astype(np.float32), u=us, history=hists)
+        print(f"[case] randomized f32 V={V} B={B}", flush=True)
+        rep = compare(run_gpu(w), run_oracle(w))
+        _report(f"randomized-f32-{V}", rep)
+        assert_parity(rep, f"randomized-f32-{V}")
+
+
 def test_bf16_special_rows_on_the_window_and_mid_paths():
     """bf16 rows of the fast kernel with +inf, -inf runs, all -inf, and a
     single finite value, under top-k 0, 100, 1000 and 5000 (the window, the
