@@ -74,6 +74,8 @@ struct DistMap {
 
 // Per-row values shared through LDS.
 struct DistExtra {
+  double dW[4];       // per range: row cumulative mass minus bucket cumulative mass
+  uint32_t dN[4];     // the same for counts
   uint32_t ctr[2];    // dist_stream's batch counters, one per pass
   uint32_t gcount;    // gathered elements
   uint32_t generic;   // set by the finishing wave: the row goes to the generic engine
@@ -280,6 +282,7 @@ __device__ __forceinline__ void wave_bitonic(uint64_t (&v)[E]) {
 // row's sorted order (through itself), weight and 1-based rank in the bucket.
 struct DistPick {
   bool found;
+  bool big;  // not resolved: the bucket holds more entries than one wave sorts
   uint64_t g;
   double c, w;
   uint32_t rank;
@@ -299,7 +302,7 @@ __device__ __forceinline__ DistPick dist_resolve_e(const uint64_t *lst, uint32_t
     v[e] = i < m ? lst[i] : ~0ull;
   }
   wave_bitonic<E>(v);
-  DistPick pk = {false, 0ull, 0.0, 0.0, 0u};
+  DistPick pk = {false, false, 0ull, 0.0, 0.0, 0u};
   double carry = 0.0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -361,7 +364,7 @@ __device__ __forceinline__ DistPick dist_resolve_small(const uint64_t *lst, doub
   const double incl = pre + w;
   const bool hit = lane < m && (want ? rank == want : (rank <= lim && base + incl >= t));
   const uint32_t best = uniform(wave_min(hit ? rank : ~0u));
-  DistPick pk = {false, 0ull, 0.0, 0.0, 0u};
+  DistPick pk = {false, false, 0ull, 0.0, 0.0, 0u};
   if (best != ~0u) {
     const uint64_t bal = __ballot(hit && rank == best);
     const int l = __builtin_ctzll(bal);
@@ -480,18 +483,17 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
   uint32_t kmax = 0u, nneg = 0u;
   const bool temp_on = c.temp_on != 0;
   const float scale = c.scale;
-  // negative NaNs count but enter no bin: their atomics go to a dummy slot
-  // (the gather buffer is unused until pass 2)
-  double *const dummy_w = (double *)&ss.gather[0];
-  uint32_t *const dummy_c = (uint32_t *)&ss.gather[1];
+  // Negative NaNs are counted and add nothing to the bin their index lands
+  // in (a valid one: the clamp of a NaN gives bin 0), so that no element
+  // branches.
   auto put1 = [&](float y, auto kon) {
     const uint32_t key = order_key(y);
     kmax = key > kmax ? key : kmax;
     const bool nan = key < TR::kNegInfKey;
     nneg += nan ? 1u : 0u;
     const uint32_t b = map.bin(y);
-    atomicAdd(nan ? dummy_w : &ss.bw[b], nan ? 0.0 : (double)map.weight(y));
-    if constexpr (decltype(kon)::value) atomicAdd(nan ? dummy_c : &ss.bcnt[b], 1u);
+    atomicAdd(&ss.bw[b], nan ? 0.0 : (double)map.weight(y));
+    if constexpr (decltype(kon)::value) atomicAdd(&ss.bcnt[b], nan ? 0u : 1u);
   };
   auto pass1 = [&](auto kon) {
     dist_stream(
@@ -655,7 +657,12 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
     atomicAdd(&bkN[bk], 1u);
     atomicAdd(&bkW[bk], (double)map.weight(y));
   };
-  auto in_ranges = [&](uint32_t key, uint32_t b) { return key >= TR::kNegInfKey && rg.of(b) >= 0; };
+  // branch-free (bitwise, not short-circuit): evaluated for every element
+  const uint32_t q_lo0 = rg.lo0, q_len0 = rg.len0, q_lo1 = rg.lo1, q_len1 = rg.len1, q_lo2 = rg.lo2,
+                 q_len2 = rg.len2;
+  auto in_ranges = [=](uint32_t key, uint32_t b) -> bool {
+    return (key >= TR::kNegInfKey) & ((b - q_lo0 < q_len0) | (b - q_lo1 < q_len1) | (b - q_lo2 < q_len2));
+  };
   dist_stream(
       row, V, v4, c.hist_on != 0, ht.bitmap, &dx.ctr[1], nullptr,
       [&](float4 d, uint32_t i0, uint32_t mb) {
@@ -718,50 +725,58 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
 
   // ---- one wave resolves the row; the others wait at the barrier below ----
   if (threadIdx.x < 64u) {
-    uint64_t *lst = (uint64_t *)sh.ht.keys;  // the history tables are no longer read
+    uint64_t *const lst = (uint64_t *)sh.ht.keys;  // the history tables are no longer read
+    double *const wl = (double *)sh.ht.counts;
+    const uint64_t *const gat = ss.gather;
     const uint32_t fb1 = off1 << lsh, fb2 = off2 << lsh;
-    auto rng = [&](uint32_t bk) -> int { return bk < fb1 ? 0 : (bk < fb2 ? 1 : 2); };
-    // row cumulative = bucket cumulative + the range's offset
-    const double dW0 = rW0, dW1 = rW1 - (fb1 ? bkW[fb1 - 1u] : 0.0), dW2 = rW2 - (fb2 ? bkW[fb2 - 1u] : 0.0);
-    const uint32_t dN0 = rN0, dN1 = rN1 - (fb1 ? bkN[fb1 - 1u] : 0u), dN2 = rN2 - (fb2 ? bkN[fb2 - 1u] : 0u);
-    auto dW = [&](uint32_t bk) -> double { const int q = rng(bk); return q == 0 ? dW0 : (q == 1 ? dW1 : dW2); };
-    auto dN = [&](uint32_t bk) -> uint32_t { const int q = rng(bk); return q == 0 ? dN0 : (q == 1 ? dN1 : dN2); };
-    auto rowW_incl = [&](uint32_t bk) -> double { return dW(bk) + bkW[bk]; };
-    auto rowW_excl = [&](uint32_t bk) -> double { return dW(bk) + (bk ? bkW[bk - 1u] : 0.0); };
-    auto count_of = [&](uint32_t bk) -> uint32_t { return bkN[bk] - (bk ? bkN[bk - 1u] : 0u); };
+    // row cumulative = bucket cumulative + the range's offset, from a table
+    // in LDS.  (A selection among locals captured by the lambdas below would
+    // put them in scratch memory.)
+    double *const tW = dx.dW;
+    uint32_t *const tN = dx.dN;
+    if ((threadIdx.x & 63u) == 0u) {
+      tW[0] = rW0;
+      tW[1] = rW1 - (fb1 ? bkW[fb1 - 1u] : 0.0);
+      tW[2] = rW2 - (fb2 ? bkW[fb2 - 1u] : 0.0);
+      tN[0] = rN0;
+      tN[1] = rN1 - (fb1 ? bkN[fb1 - 1u] : 0u);
+      tN[2] = rN2 - (fb2 ? bkN[fb2 - 1u] : 0u);
+    }
+    __builtin_amdgcn_wave_barrier();
+    auto rng = [=](uint32_t bk) -> uint32_t { return bk < fb1 ? 0u : (bk < fb2 ? 1u : 2u); };
+    auto rowW_incl = [=](uint32_t bk) -> double { return tW[rng(bk)] + bkW[bk]; };
+    auto rowW_excl = [=](uint32_t bk) -> double { return tW[rng(bk)] + (bk ? bkW[bk - 1u] : 0.0); };
+    auto rowN_incl = [=](uint32_t bk) -> uint32_t { return tN[rng(bk)] + bkN[bk]; };
+    auto rowN_excl = [=](uint32_t bk) -> uint32_t { return tN[rng(bk)] + (bk ? bkN[bk - 1u] : 0u); };
+    auto count_of = [=](uint32_t bk) -> uint32_t { return bkN[bk] - (bk ? bkN[bk - 1u] : 0u); };
     // the first non-empty bucket whose row cumulative reaches t (nbk: none)
-    auto bucket_ge = [&](double t) -> uint32_t {
-      return uniform(first_bin([&](uint32_t bk) { return bk >= nbk || (bkN[bk] > 0u && rowW_incl(bk) >= t); }));
+    auto bucket_ge = [=](double t) -> uint32_t {
+      return uniform(first_bin([=](uint32_t bk) { return bk >= nbk || (bkN[bk] > 0u && rowW_incl(bk) >= t); }));
     };
-    bool generic = false;
-    // Resolves bucket X; an empty result when the bucket holds more than the
-    // finishing wave sorts.
-    auto resolve = [&](uint32_t X, uint32_t want, double t, uint32_t lim) -> DistPick {
-      DistPick none = {false, 0ull, 0.0, 0.0, 0u};
+    // Resolves bucket X (big: it holds more entries than one wave sorts)
+    auto resolve = [=](uint32_t X, uint32_t want, double t, uint32_t lim) -> DistPick {
+      DistPick none = {false, false, 0ull, 0.0, 0.0, 0u};
       if (X >= nbk) return none;
       const uint32_t m = uniform(count_of(X));
-      if (m == 0u || m > 512u) {
-        generic = true;
-        return none;
-      }
-      const uint32_t ml = dist_list(ss.gather, n, X, lst);
-      if (ml != m) {
-        generic = true;
+      if (m == 0u || m > 512u || dist_list(gat, n, X, lst) != m) {
+        none.big = true;
         return none;
       }
       const double base = uniform(rowW_excl(X));
-      if (m <= 64u) return dist_resolve_small(lst, (double *)sh.ht.counts, m, map, want, base, t, lim);
+      if (m <= 64u) return dist_resolve_small(lst, wl, m, map, want, base, t, lim);
       return dist_resolve_big(lst, m, map, want, base, t, lim);
     };
+    bool generic = false;
 
     // the end of the top-k / min-p set: (bucket, number kept in it) and mass
     uint32_t end_bk = ~0u, end_n = 0u;
     double s_kept = totalW;
     if (e < (uint32_t)kBins) {
       if (k_part) {
-        const uint32_t X = uniform(first_bin([&](uint32_t bk) { return bk >= nbk || dN(bk) + bkN[bk] >= (uint32_t)c.top_k; }));
+        const uint32_t kk = (uint32_t)c.top_k;
+        const uint32_t X = uniform(first_bin([=](uint32_t bk) { return bk >= nbk || rowN_incl(bk) >= kk; }));
         if (X < nbk) {
-          const uint32_t want = (uint32_t)c.top_k - uniform(dN(X) + (X ? bkN[X - 1u] : 0u));
+          const uint32_t want = kk - uniform(rowN_excl(X));
           const DistPick pk = resolve(X, want, 0.0, ~0u);
           if (pk.found) {
             end_bk = X;
@@ -789,7 +804,7 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
         for (uint32_t b0 = 0u; b0 < n; b0 += 64u) {
           const uint32_t i = b0 + (threadIdx.x & 63u);
           if (i < n) {
-            const uint64_t g = ss.gather[i];
+            const uint64_t g = gat[i];
             const uint32_t key = ~(uint32_t)(g >> 32);
             if (((uint32_t)g & 0x7FFu) == Y && key >= key_mp) {
               ++cnt;
@@ -814,7 +829,8 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
       const double t = c.top_p * s_kept;
       uint32_t Z = bucket_ge(t);
       if (end_bk != ~0u && Z > end_bk) Z = end_bk;
-      const DistPick pk = Z < nbk ? resolve(Z, 0u, t, Z == end_bk ? end_n : ~0u) : DistPick{false, 0ull, 0.0, 0.0, 0u};
+      const DistPick pk = resolve(Z, 0u, t, Z == end_bk ? end_n : ~0u);
+      if (pk.big) generic = true;
       if (pk.found) {
         const double acc = pk.c / s_kept, prev = (pk.c - pk.w) / s_kept;
         double mg = c.top_p - prev;
@@ -836,7 +852,7 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
       const double t = c.u * s_keep;
       uint32_t D = bucket_ge(t);
       if (cut_bk != ~0u && D > cut_bk) D = cut_bk;
-      const DistPick pk = D < nbk ? resolve(D, 0u, t, D == cut_bk ? cut_n : ~0u) : DistPick{false, 0ull, 0.0, 0.0, 0u};
+      const DistPick pk = resolve(D, 0u, t, D == cut_bk ? cut_n : ~0u);
       if (!pk.found) {
         // the target lies beyond every gathered cumulative (rounding with u
         // within 1e-12 of 1): the generic engine applies softmax_choice's
