@@ -12,7 +12,8 @@ stream the kernels are launched on.
 
 Prints one JSON line: rows/s of the whole job, microseconds per step, the HBM
 roofline of the step (algorithmic bytes / step time against 8 TB/s; measured
-HBM traffic per launch from the committed rocprofv3 counter summary) and the
+HBM traffic per launch from the committed rocprofv3 counter summary of the
+same kernel and workload, named in traffic_source) and the
 CPU baseline: the C restatement of the reference's CPU sampler timed on this
 host's cores on a bounded sample of the same rows, whose tokens are also
 compared with the GPU's.
@@ -32,7 +33,6 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak
 LLC_BYTES = 256 << 20  # MI355X Infinity Cache (MALL)
 METRIC = "sampled rows/sec + µs/step + % HBM peak, batch 256 × vocab 128256 bf16"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_bf16_fast_kernel_C3.txt")
 
 
 def log(msg: str) -> None:
@@ -57,15 +57,27 @@ def kernel_label(w) -> str:
     if w.dtype == "bf16" and w.vocab % 8 == 0 and 0 < w.vocab <= 40 * 4096:
         nch = next(n for n in (8, 16, 32, 40) if w.vocab <= n * 4096)
         return f"bf16_fast_kernel<{nch}> (one launch per step)"
-    return f"generic_sample_kernel<{0 if w.dtype == 'bf16' else 2}> (one launch per step)"
+    if w.dtype == "bf16":
+        return "generic_sample_kernel<0> (one launch per step)"
+    return "f32_sample_kernel (one launch per step)"
 
 
-def read_traffic(name: str):
-    """HBM bytes per launch from the committed counter summary (None if absent)."""
-    if name != "C3" or not os.path.exists(TRAFFIC_FILE):
-        return None
-    m = re.search(r"^traffic_bytes_per_launch\s*=\s*([0-9.]+)", open(TRAFFIC_FILE).read(), re.M)
-    return float(m.group(1)) if m else None
+def traffic_file(w) -> str:
+    """The committed counter summary of this workload's kernel (profiles/)."""
+    kernel = kernel_label(w).split("<")[0].split(" ")[0]
+    suffix = "_generic" if (w.name == "C3" and w.vocab != 128256) else ""
+    return os.path.join(ROOT, "profiles", f"traffic_{kernel}_{w.name}{suffix}.txt")
+
+
+def read_traffic(w):
+    """HBM bytes per launch from the committed counter summary of the same
+    kernel and workload (rocprofv3 FETCH_SIZE and WRITE_SIZE runs, scaled by
+    a device copy's counters); None if absent."""
+    path = traffic_file(w)
+    if not os.path.exists(path):
+        return None, None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*([0-9.]+)", open(path).read(), re.M)
+    return (float(m.group(1)) if m else None), os.path.relpath(path, ROOT)
 
 
 def cpu_baseline(w, gpu_out, seconds: float):
@@ -178,6 +190,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="C3", choices=["C1", "C2", "C3", "C4", "C5"])
+    ap.add_argument("--vocab", type=int, default=0,
+                    help="keep only the first VOCAB logits of every row (e.g. an odd vocab on C3 runs the "
+                         "generic bf16 kernel); a parity and counter case, not the metric")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--copy-calibration", type=int, metavar="MB", default=0,
@@ -206,7 +221,9 @@ def main() -> int:
 
     S.lib()  # fails loudly when the HIP library is not built
     w = W.CONFIGS[args.config]()
-    log(f"bench: {args.config} batch {w.batch} vocab {w.vocab} {w.dtype}")
+    if args.vocab:
+        w = w.truncated(args.vocab)
+    log(f"bench: {args.config} batch {w.batch} vocab {w.vocab} {w.dtype} ({kernel_label(w)})")
     dev = torch.device("cuda", 0)
     if w.dtype == "bf16":
         import numpy as np
@@ -272,7 +289,7 @@ def main() -> int:
     }
     alg = w.algorithmic_bytes()
     achieved = alg / (ms * 1e-3) / 1e9
-    traffic = read_traffic(w.name)
+    traffic, traffic_src = read_traffic(w)
     line = {
         "metric": METRIC,
         "value": w.batch / (ms * 1e-3),
@@ -291,7 +308,7 @@ def main() -> int:
         "data": "synthetic (seeded generator of the configuration's distributions)",
         "config": workload_config(w),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
                      "algorithmic_bytes": alg, "kernel": kernel_label(w)},
         "rotating_buffers": nrot,
         # secondary denominator: the measured read rate of the same rotating

@@ -15,7 +15,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblmrs_sampling.so")
 
-SOURCES = ["sampling_api.hip"]
+# one translation unit per kernel family, compiled in parallel, then linked
+SOURCES = ["sampling_api.hip", "fast_nch8.hip", "fast_nch16.hip", "fast_nch32.hip", "fast_nch40.hip",
+           "generic_kernels.hip", "f32_kernel.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -47,9 +49,7 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
-def _build_one(sources, lib, verbose):
-    srcs = [os.path.join(CSRC, s) for s in sources]
-    cmd = [HIPCC, *FLAGS, "-I", os.path.join(ROOT, "include"), *srcs, "-o", lib + ".tmp"]
+def _run(cmd, verbose, what):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -57,9 +57,24 @@ def _build_one(sources, lib, verbose):
     errs = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
     if res.returncode != 0:
         sys.stderr.write("\n".join(errs) + "\n")
-        raise RuntimeError(f"hipcc failed ({res.returncode}) building {lib}")
+        raise RuntimeError(f"hipcc failed ({res.returncode}) building {what}")
     if verbose and errs:
         sys.stderr.write("\n".join(errs) + "\n")
+
+
+def _build_one(sources, lib, verbose):
+    from concurrent.futures import ThreadPoolExecutor
+
+    inc = ["-I", os.path.join(ROOT, "include")]
+    cflags = [f for f in FLAGS if f != "-shared"]
+    objs = [lib + f".{os.path.splitext(s)[0]}.o" for s in sources]
+    jobs = [([HIPCC, *cflags, *inc, "-c", os.path.join(CSRC, s), "-o", o], o) for s, o in zip(sources, objs)]
+    with ThreadPoolExecutor(max_workers=min(len(jobs), os.cpu_count() or 1)) as ex:
+        for f in [ex.submit(_run, cmd, verbose, o) for cmd, o in jobs]:
+            f.result()
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", lib + ".tmp"], verbose, lib)
+    for o in objs:
+        os.remove(o)
     os.replace(lib + ".tmp", lib)
 
 

@@ -876,6 +876,66 @@ __device__ __forceinline__ uint32_t find_jth_regs(FastShared &sh, const uint32_t
   });
 }
 
+// The ordered search for a tie group of at most kListCap elements: every
+// element whose z key lies in [lo, hi] (members by their z key, the others
+// by the raw key in registers) is listed in LDS by its index, and the one
+// with exactly j - 1 smaller listed indices is the j-th.  The register pass
+// tests a chunk's eight keys with packed 16-bit subtractions and minima; the
+// few chunks that hold a match list their elements.  The caller has cleared
+// counters()[kCtrList] before its last barrier; every key in [lo, hi] is
+// above the padding's -inf (lo > kNegInfKey16).
+constexpr int kListCap = kFT;
+constexpr int kCtrList = 2;
+constexpr int kOffList = 4096;  // inside the SelState region, free after the window
+template <int NCH>
+__device__ __forceinline__ uint32_t find_jth_list(FastShared &sh, const uint32_t (&k)[NCH][4], uint32_t nmem,
+                                                  bool hist, uint32_t lo, uint32_t hi, uint32_t j) {
+  const int tid = threadIdx.x;
+  uint32_t *list = sh.u32(kOffList), *ctr = &sh.counters()[kCtrList];
+  const uint32_t *midx = sh.m_idx(), *mkey = sh.m_key();
+  const u16x2 lo2 = {(unsigned short)lo, (unsigned short)lo};
+  const uint32_t span = hi - lo;
+  auto put = [&](uint32_t idx) {
+    const uint32_t p = atomicAdd(ctr, 1u);
+    if (p < (uint32_t)kListCap) list[p] = idx;
+  };
+  const int ft = fresh_tid();
+  static_for<0, NCH>([&](auto S) {
+    constexpr int s = decltype(S)::value;
+    // key - lo per 16-bit half (wrapping: keys below lo become large)
+    uint32_t d[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t kq = k[s][q];  // (copied to a scalar before the cast)
+      d[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, kq) - lo2);
+    }
+    const uint32_t m = pk_min_u16(pk_min_u16(d[0], d[1]), pk_min_u16(d[2], d[3]));
+    if (min(m & 0xFFFFu, m >> 16) <= span) {
+      const uint32_t ch = (uint32_t)(s * kFT + ft);
+      uint32_t m8 = 0u;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m8 |= (((d[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu) <= span ? 1u : 0u) << e;
+      if (hist) m8 &= ~chunk_m8(sh, ch);  // members enter by their z key
+      for (; m8; m8 &= m8 - 1u) put(ch * 8u + (uint32_t)__builtin_ctz(m8));
+    }
+  });
+  for (uint32_t m = (uint32_t)tid; m < nmem; m += kFT) {
+    const uint32_t zk = mkey[m] >> 16;
+    if (zk >= lo && zk <= hi) put(midx[m]);
+  }
+  if (tid == 0) sh.bsel[5] = 0xFFFFFFFFu;  // (no j-th element: the caller falls back)
+  __syncthreads();
+  const uint32_t n = min(uniform(*ctr), (uint32_t)kListCap);
+  if ((uint32_t)tid < n) {
+    const uint32_t v = list[tid];
+    uint32_t below = 0u;
+    for (uint32_t q = 0; q < n; ++q) below += list[q] < v ? 1u : 0u;
+    if (below + 1u == j) sh.bsel[5] = v;
+  }
+  __syncthreads();
+  return uniform(sh.bsel[5]);
+}
+
 // ---- the full distribution from the window of top keys ----------------------------
 //
 // A row's mass sits in its top keys: the window pass counts, by LDS atomics
@@ -897,7 +957,11 @@ constexpr int kOffWinHist = 4096;              // views inside the SelState regi
 constexpr int kOffWinKey = kOffWinHist + kWin * 4;
 constexpr int kOffWinCnt = kOffWinKey + kWin * 4;
 constexpr int kOffWinMass = kOffWinCnt + kWin * 4;
-static_assert(kOffTcnt + kFT * 4 <= kOffWinHist && kOffWinMass + kWin * 8 <= kOffWhist, "window views");
+constexpr int kOffWinList = 16 * 1024;          // the listed chunks' keys, then their indices
+constexpr int kWinListCap = 2048;
+constexpr int kOffWinListCh = kOffWinList + kWinListCap * 16;
+static_assert(kOffTcnt + kFT * 4 <= kOffWinHist && kOffWinMass + kWin * 8 <= kOffWinList &&
+              kOffWinListCh + kWinListCap * 4 <= kOffWhist, "window views");
 
 // Returns false (uniformly, with the registers and the member list intact)
 // when the row needs the 65536-bin path.
@@ -916,13 +980,22 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   // zlow_max is an element's z key: its y is at most the row's maximum; the
   // chunks whose largest z key lies below zskip hold only weights below e^-kSkip
   const float ys = key16_value(temp_key16(zlow_max, c)) - kSkip;
-  uint32_t zskip = zlow_max;  // the lowest key whose y reaches ys (zlow_max's does)
-  for (uint32_t lo = kNegInfKey16; lo < zskip;) {
-    const uint32_t mid = lo + ((zskip - lo) >> 1);
-    if (key16_value(temp_key16(mid, c)) >= ys)
-      zskip = mid;
-    else
-      lo = mid + 1u;
+  // the lowest key whose y reaches ys (zlow_max's does): a search over the
+  // lanes, each round testing 64 keys spread over the range left (at most
+  // four rounds over the 16-bit keys)
+  uint32_t zskip = zlow_max;
+  {
+    const uint32_t lane = (uint32_t)tid & 63u;
+    uint32_t lo = kNegInfKey16;  // the answer lies in [lo, zskip]
+    while (lo < zskip) {
+      const uint32_t step = (zskip - lo + 62u) / 63u;  // lane 63 tests zskip itself
+      const uint32_t kk = min(lo + lane * step, zskip);
+      const uint64_t ok = __ballot(key16_value(temp_key16(kk, c)) >= ys);
+      const uint32_t f = (uint32_t)__builtin_ctzll(ok);  // ok has lane 63
+      const uint32_t hi = min(lo + f * step, zskip);
+      lo = f ? lo + (f - 1u) * step + 1u : lo;
+      zskip = hi;
+    }
   }
   zlo = max(zlo, zskip);  // keys below zskip are neither counted nor summed
   // every element below the window weighs less than e^-kSkip: a cut that
@@ -933,26 +1006,59 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   const float l2e = 1.4426950408889634f, mb2 = Mb * l2e;
   uint32_t *wh = sh.u32(kOffWinHist);
   wh[tid] = 0u;
-  __syncthreads();
-  double below = 0.0;
+  // One chunk's window counts (by LDS atomics) and the weight sum of its
+  // elements below the window.
+  auto window_chunk = [&](const uint4 &w, uint32_t ch) {
+    const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+    const uint32_t m8 = hist ? chunk_m8(sh, ch) : 0u;  // members enter by their z key
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t key = (x[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
+      const bool mem = (m8 >> e) & 1u;
+      if (!mem && key >= zlo) atomicAdd(&wh[zhb - key], 1u);
+      const float wt = __builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(key, c)), l2e, -mb2));
+      acc += (mem || key >= zlo || key < zskip) ? 0.0f : wt;
+    }
+    return acc;
+  };
+  // The chunks with a key at or above zskip (the others are skipped).  When
+  // the window reaches zskip (heavy-tailed rows) they are usually few: then
+  // they are listed in LDS first, so that each thread takes about one;
+  // otherwise every thread works through its own slots.  The scan's
+  // barriers also order the histogram's clear.
   const int ft = fresh_tid();
+  uint64_t live = 0u;
   static_for<0, NCH>([&](auto S) {
     constexpr int s = decltype(S)::value;
-    const int ch = s * kFT + ft;
-    if (ch < nchunks && chunk_max(k[s]) >= zskip) {
-      const uint32_t m8 = hist ? chunk_m8(sh, (uint32_t)ch) : 0u;  // members enter by their z key
-      float acc = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t key = (k[s][e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-        const bool mem = (m8 >> e) & 1u;
-        if (!mem && key >= zlo) atomicAdd(&wh[zhb - key], 1u);
-        const float w = __builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(key, c)), l2e, -mb2));
-        acc += (mem || key >= zlo || key < zskip) ? 0.0f : w;
-      }
-      below += (double)acc;
-    }
+    live |= (uint64_t)((s * kFT + ft < nchunks && chunk_max(k[s]) >= zskip) ? 1u : 0u) << s;
   });
+  uint32_t nlive = 0xFFFFFFFFu, lpos = 0u;
+  if (tail_negligible)
+    lpos = block_exclusive_scan<kFW>((uint32_t)__builtin_popcountll(live), sh.uscr, &nlive);
+  else
+    __syncthreads();
+  double below = 0.0;
+  if (nlive <= (uint32_t)kWinListCap) {
+    uint4 *lk = (uint4 *)sh.u32(kOffWinList);
+    uint32_t *lc = sh.u32(kOffWinListCh), p = lpos;
+    static_for<0, NCH>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      if ((live >> s) & 1u) {
+        lk[p] = make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]);
+        lc[p] = (uint32_t)(s * kFT + ft);
+        ++p;
+      }
+    });
+    __syncthreads();
+    for (uint32_t i = (uint32_t)tid; i < nlive; i += kFT) below += (double)window_chunk(lk[i], lc[i]);
+  } else {
+    static_for<0, NCH>([&](auto S) {
+      constexpr int s = decltype(S)::value;
+      if ((live >> s) & 1u)
+        below += (double)window_chunk(make_uint4(k[s][0], k[s][1], k[s][2], k[s][3]), (uint32_t)(s * kFT + ft));
+    });
+  }
   for (uint32_t m = tid; m < nmem; m += kFT) {
     const uint32_t zk = mkey[m] >> 16;
     if (zk >= zlo)
@@ -1102,10 +1208,13 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   if (jj > (double)gmax) jj = (double)gmax;
   const uint32_t jt = (uint32_t)jj;
   const uint32_t zhi = uniform(ekey[h]), zlo2 = uniform(ekey[tl]);
+  const uint32_t gtot = uniform(cincl[tl] - cnt_excl(h));  // the group's elements
   const float yv = key16_value(ykey_of(h));
   const bool first_tok = (h == 0 && jt == 1u), last_tok = (h == last_h && jt == gmax);
+  if (tid == 0) sh.counters()[kCtrList] = 0u;
   __syncthreads();  // the window views are dead
-  const uint32_t token = find_jth_regs<NCH>(sh, k, nchunks, nmem, zlo2, zhi, jt);
+  uint32_t token = gtot <= (uint32_t)kListCap ? find_jth_list<NCH>(sh, k, nmem, hist, zlo2, zhi, jt) : ~0u;
+  if (token == ~0u) token = find_jth_regs<NCH>(sh, k, nchunks, nmem, zlo2, zhi, jt);
   if (tid == 0) {
     const double lo_c = (mx2 + (double)(jt - 1u) * wg) / kept_mass, hi_c = lo_c + wg / kept_mass;
     double m = 1.0;

@@ -89,29 +89,43 @@ __device__ inline RowCfg uniform_cfg(const RowCfg &s) {
 // LMRS_GREEDY invalid.  Greedy rows carry top_k = 1 with `greedy` set.
 // With strategy == false (the processor chain alone) the top-k, top-p and
 // min-p fields are neither read nor checked.
+// Row parameters are read through the constant address space: the arrays
+// are never written while a kernel runs, so the compiler reads them with
+// scalar loads, all issued together and waited for on the scalar counter,
+// without waiting for the row's vector loads in flight (as vector loads they
+// would be read one at a time, each behind every row load issued before it).
+// A NULL array reads its neutral value from kNeutral* (no branch between the
+// loads).
+template <class T>
+__device__ __forceinline__ T param_load(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)p;
+}
+__device__ const float kNeutralRep = 1.0f, kNeutralZeroF = 0.0f;
+__device__ const double kNeutralOneD = 1.0, kNeutralMinP = -1.0, kNeutralZeroD = 0.0;
+__device__ const int32_t kNeutralTopK = 0;
+__device__ const int64_t kNeutralOffsets[2] = {0, 0};
+
 __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtype, bool strategy = true) {
   RowCfg c;
   c.status = LMRS_ROW_OK;
-  float rep = a.repetition_penalty ? a.repetition_penalty[r] : 1.0f;
-  float pres = a.presence_penalty ? a.presence_penalty[r] : 0.0f;
-  float freq = a.frequency_penalty ? a.frequency_penalty[r] : 0.0f;
-  double t = a.temperature ? a.temperature[r] : 1.0;
-  int64_t k = strategy && a.top_k ? (int64_t)a.top_k[r] : 0;
-  double p = strategy && a.top_p ? a.top_p[r] : 1.0;
-  double mp = strategy && a.min_p ? a.min_p[r] : -1.0;
-  c.u = strategy && a.uniforms ? a.uniforms[r] : 0.0;
+  const float rep = param_load(a.repetition_penalty ? a.repetition_penalty + r : &kNeutralRep);
+  const float pres = param_load(a.presence_penalty ? a.presence_penalty + r : &kNeutralZeroF);
+  const float freq = param_load(a.frequency_penalty ? a.frequency_penalty + r : &kNeutralZeroF);
+  const double t = param_load(a.temperature ? a.temperature + r : &kNeutralOneD);
+  const int64_t k = (int64_t)param_load(strategy && a.top_k ? a.top_k + r : &kNeutralTopK);
+  const double p = param_load(strategy && a.top_p ? a.top_p + r : &kNeutralOneD);
+  const double mp = param_load(strategy && a.min_p ? a.min_p + r : &kNeutralMinP);
+  c.u = param_load(strategy && a.uniforms ? a.uniforms + r : &kNeutralZeroD);
+  const int64_t *offs = a.hist_offsets ? a.hist_offsets + r : kNeutralOffsets;
+  const int64_t h0 = param_load(offs), h1 = param_load(offs + 1);
   if (!(__builtin_isfinite(rep) && rep > 0.0f) || !__builtin_isfinite(pres) ||
       !__builtin_isfinite(freq) || !(__builtin_isfinite(t) && t > 0.0) || k < LMRS_GREEDY ||
       !(__builtin_isfinite(p) && p > 0.0 && p <= 1.0) || __builtin_isnan(mp) || mp > 1.0)
     c.status = LMRS_ROW_PARAM;
-  c.h_begin = 0;
-  c.h_len = 0;
-  if (a.hist_offsets) {
-    c.h_begin = a.hist_offsets[r];
-    c.h_len = a.hist_offsets[r + 1] - c.h_begin;
-    if (c.h_len < 0) c.status = LMRS_ROW_PARAM;
-    if (c.h_len > LMRS_MAX_HISTORY && c.status == LMRS_ROW_OK) c.status = LMRS_ROW_HISTORY;
-  }
+  c.h_begin = h0;
+  c.h_len = h1 - h0;
+  if (c.h_len < 0) c.status = LMRS_ROW_PARAM;
+  if (c.h_len > LMRS_MAX_HISTORY && c.status == LMRS_ROW_OK) c.status = LMRS_ROW_HISTORY;
   const bool has_hist = c.h_len > 0;
   c.rep_on = (rep != 1.0f) && has_hist;                        // repetition.rs:82-84
   c.pres_on = has_hist && !(pres == 0.0f && freq == 0.0f);     // presence.rs:102-104
@@ -150,7 +164,8 @@ __device__ __forceinline__ bool minp_keeps(float l, double thr) { return exp((do
 // and the device's exp to agree on its side (each is within an ulp or two of
 // the exact value); logits equal to the maximum compare exp(max) with itself.
 __device__ __forceinline__ bool minp_near(float l, float max, double thr) {
-  if (l == max || __builtin_isnan(l) || !__builtin_isfinite(thr)) return false;
+  // a zero threshold (exp(max) underflows) keeps every logit on both sides
+  if (l == max || __builtin_isnan(l) || !__builtin_isfinite(thr) || !(thr > 0.0)) return false;
   const double e = exp((double)l);
   return fabs(e - thr) <= 1e-12 * thr + 1e-300;
 }

@@ -1,11 +1,10 @@
 // sampling_api.hip -- the C-ABI entry points (include/lmrs_sampling.h).
 //
 // Host-side argument checks, then one launch of one workgroup per row on the
-// caller's stream.  Nothing here allocates device memory.
+// caller's stream (the kernels live in their own translation units, behind
+// launch.hpp).  Nothing here allocates device memory.
 #include "lmrs_sampling.h"
-#include "f32_dist.hpp"
-#include "fast_bf16.hpp"
-#include "generic_engine.hpp"
+#include "launch.hpp"
 
 namespace {
 
@@ -36,23 +35,24 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
   hipStream_t s = (hipStream_t)stream;
   const int vec = vector_ok(args);
   const int64_t V = args->vocab;
-  if (args->dtype == LMRS_DTYPE_BF16 && vec && V > 0 && V % 8 == 0 && V <= lmrs::kFastMaxVocab) {
-    // register-resident rows: NCH chunks of 8 logits per thread (rows the
-    // fast path does not take finish in the generic engine, in the same launch)
-    const dim3 grid(args->batch), block(lmrs::kFT);
-    constexpr int kSlot = 8 * lmrs::kFT;  // logits per chunk slot (one 16-byte chunk per thread)
+  // register-resident bf16 rows: NCH slots of one 16-byte chunk (eight
+  // logits) per thread of a 512-thread workgroup (rows the fast kernel does
+  // not take finish in the generic engine, in the same launch)
+  constexpr int64_t kSlot = lmrs::kFastSlotLogits;
+  if (args->dtype == LMRS_DTYPE_BF16 && vec && V > 0 && V % 8 == 0 && V <= lmrs::kFastVocabMax) {
     if (V <= 8 * kSlot)
-      lmrs::bf16_fast_kernel<8><<<grid, block, 0, s>>>(*args);
+      lmrs::launch_fast_bf16_8(*args, s);
     else if (V <= 16 * kSlot)
-      lmrs::bf16_fast_kernel<16><<<grid, block, 0, s>>>(*args);
+      lmrs::launch_fast_bf16_16(*args, s);
     else if (V <= 32 * kSlot)
-      lmrs::bf16_fast_kernel<32><<<grid, block, 0, s>>>(*args);
+      lmrs::launch_fast_bf16_32(*args, s);
     else
-      lmrs::bf16_fast_kernel<lmrs::kMaxSlots><<<grid, block, 0, s>>>(*args);
-  } else if (args->dtype == LMRS_DTYPE_BF16)
-    lmrs::generic_sample_kernel<LMRS_DTYPE_BF16><<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
-  else
-    lmrs::f32_sample_kernel<<<args->batch, lmrs::kThreads, 0, s>>>(*args, vec);
+      lmrs::launch_fast_bf16_40(*args, s);
+  } else if (args->dtype == LMRS_DTYPE_BF16) {
+    lmrs::launch_generic_bf16(*args, vec, s);
+  } else {
+    lmrs::launch_f32(*args, vec, s);
+  }
   return hipGetLastError() == hipSuccess ? LMRS_OK : LMRS_ERR_LAUNCH;
 }
 
@@ -60,11 +60,7 @@ extern "C" int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, 
   const int st = check_args(args, false);
   if (st != LMRS_OK || args->batch == 0 || args->vocab == 0) return st;
   if (!out) return LMRS_ERR_NULL_ARGUMENT;
-  hipStream_t s = (hipStream_t)stream;
-  if (args->dtype == LMRS_DTYPE_BF16)
-    lmrs::process_kernel<LMRS_DTYPE_BF16><<<args->batch, lmrs::kThreads, 0, s>>>(*args, out);
-  else
-    lmrs::process_kernel<LMRS_DTYPE_F32><<<args->batch, lmrs::kThreads, 0, s>>>(*args, out);
+  lmrs::launch_process(*args, out, (hipStream_t)stream);
   return hipGetLastError() == hipSuccess ? LMRS_OK : LMRS_ERR_LAUNCH;
 }
 

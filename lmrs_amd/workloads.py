@@ -93,6 +93,15 @@ class Workload:
                         self.uniforms[rows], off, ids, dict(self.notes),
                         None if self.min_p is None else self.min_p[rows])
 
+    def truncated(self, vocab: int) -> "Workload":
+        """The same rows cut to their first `vocab` logits (history ids beyond
+        it stay: the sampler ignores ids >= vocab)."""
+        if not 0 < vocab <= self.vocab:
+            raise ValueError(f"vocab {vocab} outside 1..{self.vocab}")
+        return Workload(self.name, np.ascontiguousarray(self.logits[:, :vocab]), self.repetition_penalty,
+                        self.presence_penalty, self.frequency_penalty, self.temperature, self.top_k, self.top_p,
+                        self.uniforms, self.hist_offsets, self.hist_ids, dict(self.notes, vocab=vocab), self.min_p)
+
 
 def _params(B, rep=1.0, pres=0.0, freq=0.0, t=1.0, k=0, p=1.0):
     full = lambda v, dt: np.full(B, v, dtype=dt)  # noqa: E731

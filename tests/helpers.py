@@ -70,6 +70,17 @@ def compare(gpu, ref):
     rel = np.abs(prob_gpu - ref["prob"]) / np.maximum(ref["prob"], 1e-300)
     rel = np.where(both, rel, 0.0)
     logit_bad = int(np.sum(both & (gpu["logit"].view(np.uint32) != ref["logit"].view(np.uint32))))
+    # The GPU's near-boundary flag against the oracle's margins: rows well
+    # inside the margin must carry it, rows well outside must not (the two
+    # compute their sums in different orders, so a band around the margin
+    # itself is left to either side).  Rows with a min-p cut are only checked
+    # one way: the GPU tests the keys on both sides of the cut whether or not
+    # an element holds them, so it may flag a row whose elements all lie
+    # clear of the threshold.
+    flag = (gpu["status"] & 0x100) != 0
+    mg = np.minimum(ref["cdf_margin"], ref["top_p_margin"])
+    must = ok & ((mg < 0.5 * BOUNDARY) | (ref["min_p_margin"] < 0.5 * MINP_BOUNDARY))
+    must_not = ok & (mg > 2 * BOUNDARY) & np.isinf(ref["min_p_margin"])
     return {
         "rows": int(len(ok)),
         "status_mismatch": status_mismatch,
@@ -79,6 +90,8 @@ def compare(gpu, ref):
         "gpu_flagged": int(np.sum((gpu["status"] & 0x100) != 0)),
         "max_prob_rel_err": float(np.max(rel)) if len(rel) else 0.0,
         "logit_mismatch": logit_bad,
+        "flag_missing": int(np.sum(must & ~flag)),
+        "flag_extra": int(np.sum(must_not & flag)),
         "mismatch_rows": np.nonzero(mism)[0][:10].tolist(),
     }
 
@@ -88,3 +101,4 @@ def assert_parity(rep, name=""):
     assert rep["token_mismatch"] == 0, (name, rep)
     assert rep["logit_mismatch"] == 0, (name, rep)
     assert rep["max_prob_rel_err"] < PROB_RTOL, (name, rep)
+    assert rep["flag_missing"] == 0 and rep["flag_extra"] == 0, (name, rep)

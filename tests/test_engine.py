@@ -28,8 +28,10 @@ def test_sampler_for_mapping():
         E.sampler_for(E.GenerationConfig(temperature=float("nan")))  # Temperature::new(NaN)
 
 
-@pytest.mark.gpu
-def test_decode_steps_match_the_oracle_row_by_row():
+def _decode_vs_oracle(configs, steps=3, V=50000, seed=5):
+    """Runs `steps` decode steps of one DecodeBatch over sequences with the
+    given GenerationConfigs and compares every step, row by row, with the
+    oracle fed the same parameters, histories and uniforms."""
     torch = pytest.importorskip("torch")
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
@@ -37,14 +39,10 @@ def test_decode_steps_match_the_oracle_row_by_row():
     from lmrs_amd import workloads as W
 
     S.lib()
-    rng = np.random.default_rng(5)
-    V = 50000
-    configs = [E.GenerationConfig(8, 1.0, 1.0, None), E.GenerationConfig(8, 0.7, 1.0, 20),
-               E.GenerationConfig(8, 1.3, 0.9, None), E.GenerationConfig(8, 1.0, 0.5, 5),
-               E.GenerationConfig(8, 0.5, 1.0, None)]
+    rng = np.random.default_rng(seed)
     seqs = [E.SequenceState(c, seed=11 + i) for i, c in enumerate(configs)]
     batch = E.DecodeBatch(seqs)
-    for step in range(3):
+    for step in range(steps):
         x = rng.normal(0, 2, (len(seqs), 1, V)).astype(np.float32)
         bits = W.f32_to_bf16_bits(x.reshape(len(seqs), V))
         states = [s.rng for s in seqs]
@@ -69,6 +67,30 @@ def test_decode_steps_match_the_oracle_row_by_row():
         assert rep["token_mismatch"] == 0 and rep["status_mismatch"] == 0 and rep["logit_mismatch"] == 0, rep
         for s, st in zip(seqs, states):  # the RNG advances only for rows that draw
             assert s.rng == (S.next_unit(st)[1] if s.params.stochastic else st)
+    return seqs
+
+
+@pytest.mark.gpu
+def test_decode_steps_match_the_oracle_row_by_row():
+    _decode_vs_oracle([E.GenerationConfig(8, 1.0, 1.0, None), E.GenerationConfig(8, 0.7, 1.0, 20),
+                       E.GenerationConfig(8, 1.3, 0.9, None), E.GenerationConfig(8, 1.0, 0.5, 5),
+                       E.GenerationConfig(8, 0.5, 1.0, None)])
+
+
+@pytest.mark.gpu
+def test_wire_params_widened_from_f32_through_decode_steps():
+    """Requests carry T and top_p as f32 (openai.rs:160-182); the server widens
+    them to f64 (server/engine.rs:115-122), so T = 0.7 samples with
+    0.699999988079071 and top_p = 0.9 with 0.8999999761581421.  The decode
+    steps must match the oracle fed those widened values."""
+    reqs = [{"temperature": 0.7, "top_p": 0.9}, {"temperature": 0.7, "top_k": 40},
+            {"temperature": 1.1, "top_p": 0.95}, {"top_p": 0.3}, {"temperature": 0.35},
+            {"temperature": 0.7, "top_p": 0.9, "top_k": 1}, {}]
+    cfgs = [E.GenerateParams.from_request(r).to_generation_config() for r in reqs]
+    assert cfgs[0].temperature == float(np.float32(0.7)) == 0.699999988079071
+    assert cfgs[0].top_p == float(np.float32(0.9))
+    seqs = _decode_vs_oracle(cfgs, steps=4, V=128256, seed=17)
+    assert seqs[0].params.temperature == 0.699999988079071
 
 
 @pytest.mark.gpu

@@ -17,14 +17,25 @@ def asm(tmp_path_factory):
     sys.path.insert(0, ROOT)
     from lmrs_amd import build
 
-    out = tmp_path_factory.mktemp("isa") / "sampling.s"
+    from concurrent.futures import ThreadPoolExecutor
+
+    tmp = tmp_path_factory.mktemp("isa")
     flags = [f for f in build.FLAGS if f not in ("-fPIC", "-shared")]
-    cmd = [build.HIPCC, *flags, "--cuda-device-only", "-S", "-I", os.path.join(ROOT, "include"),
-           os.path.join(build.CSRC, "sampling_api.hip"), "-o", str(out)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        pytest.skip(f"hipcc unavailable or failed: {res.stderr[-300:]}")
-    return out.read_text()
+    srcs = [s for s in build.SOURCES if s.startswith("fast_nch")]
+
+    def one(src):
+        out = tmp / (src + ".s")
+        cmd = [build.HIPCC, *flags, "--cuda-device-only", "-S", "-I", os.path.join(ROOT, "include"),
+               os.path.join(build.CSRC, src), "-o", str(out)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        return res, out
+
+    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        results = list(ex.map(one, srcs))
+    for res, _ in results:
+        if res.returncode != 0:
+            pytest.skip(f"hipcc unavailable or failed: {res.stderr[-300:]}")
+    return "\n".join(out.read_text() for _, out in results)
 
 
 def test_fast_kernels_have_no_load_hazards(asm):
