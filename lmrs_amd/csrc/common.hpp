@@ -215,4 +215,20 @@ __device__ __forceinline__ int xcd_spread_row(int b, int n) {
   return (g << 3) | ((b & 7) ^ (g & 7));
 }
 
+// The rows of slots in rounds of G: slot s runs on the CU of slot s mod G
+// (a persistent workgroup's slots s, s + G, ...; with one workgroup per row
+// and G = the CU count, MI355X's dispatcher gave CU c exactly the workgroups
+// c, c + 256, ... of a 1024-row launch, one workgroup per CU fitting its
+// LDS).  Every other round takes its rows in reverse order, so that the rows
+// of one CU come from both ends of each pair of rounds: alternating and
+// half-and-half batches of cheap and costly rows (C4's greedy and
+// multinomial rows) give every CU the same mix.  Within a round, the XCD
+// spread as above.  A bijection from slots [0, n) to rows.
+constexpr int kRoundWGs = 256;  // MI355X CUs: the rounds of a launch of one workgroup per row
+__device__ __forceinline__ int round_row(int slot, int n, int G) {
+  const int x = xcd_spread_row(slot, n);
+  const int base = x / G * G;
+  if ((x / G) % 2 == 0 || base + G > n) return x;
+  return base + (G - 1) - (x - base);
+}
 }  // namespace lmrs

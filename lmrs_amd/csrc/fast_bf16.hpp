@@ -2265,13 +2265,48 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   return true;
 }
 
+__device__ __forceinline__ void launder_args(lmrs_sample_args &a) {
+  asm volatile("" : "+s"(a.logits), "+s"(a.dtype), "+s"(a.batch), "+s"(a.vocab), "+s"(a.row_stride));
+  asm volatile("" : "+s"(a.hist_offsets), "+s"(a.hist_ids), "+s"(a.repetition_penalty), "+s"(a.presence_penalty));
+  asm volatile("" : "+s"(a.frequency_penalty), "+s"(a.temperature), "+s"(a.top_k), "+s"(a.top_p));
+  asm volatile("" : "+s"(a.uniforms), "+s"(a.min_p), "+s"(a.token_ids), "+s"(a.log_probs));
+  asm volatile("" : "+s"(a.logits_out), "+s"(a.status));
+}
+
+// One workgroup per row (the rows in rounds of kRoundWGs, see round_row).
 template <int NCH>
 __global__ void __launch_bounds__(kFT) bf16_fast_kernel(lmrs_sample_args a) {
   __shared__ FastOrGeneric sh;
-  const int r = xcd_spread_row((int)blockIdx.x, (int)gridDim.x);
+  const int r = round_row((int)blockIdx.x, (int)gridDim.x, kRoundWGs);
   if (fast_row<NCH>(sh.f, a, r)) return;
   __syncthreads();
   generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, a, r, 1);
+}
+
+// A persistent launch for batches of more rows than CUs: gridDim.x
+// workgroups (one per CU) take the rows in rounds (round_row); every
+// workgroup leaves after its last row, and every wave of it runs the same
+// barriers per row.  MI355X's in-order dispatch of one workgroup per row
+// left CUs idle for up to 46 us between rows when another XCD had no CU
+// free; the loop costs register spills (hence only where it pays: the
+// widest rows, C4's shape).
+template <int NCH>
+__global__ void __launch_bounds__(kFT) bf16_fast_rounds_kernel(lmrs_sample_args a) {
+  __shared__ FastOrGeneric sh;
+  const int G = (int)gridDim.x;
+  for (int slot = (int)blockIdx.x; slot < a.batch; slot += G) {
+    const int r = round_row(slot, a.batch, G);
+    // The arguments pass through an empty asm statement at every row: what
+    // the row derives from them is computed inside the loop, not hoisted out
+    // of it and held in registers across the rows (fewer spills).
+    lmrs_sample_args ar = a;
+    launder_args(ar);
+    if (!fast_row<NCH>(sh.f, ar, r)) {
+      __syncthreads();
+      generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, ar, r, 1);
+    }
+    __syncthreads();  // the row's LDS views are dead
+  }
 }
 
 }  // namespace lmrs

@@ -6,8 +6,11 @@ namespace lmrs {
 
 static_assert(kFastSlotLogits == 8 * kFT && kFastVocabMax == kFastMaxVocab, "dispatch rule of sampling_api.hip");
 
-void launch_fast_bf16_40(const lmrs_sample_args &a, hipStream_t s) {
-  bf16_fast_kernel<40><<<dim3(a.batch), dim3(kFT), 0, s>>>(a);
+void launch_fast_bf16_40(const lmrs_sample_args &a, int grid, hipStream_t s) {
+  if (grid < a.batch)
+    bf16_fast_rounds_kernel<40><<<dim3(grid), dim3(kFT), 0, s>>>(a);
+  else
+    bf16_fast_kernel<40><<<dim3(a.batch), dim3(kFT), 0, s>>>(a);
 }
 
 }  // namespace lmrs

@@ -1,8 +1,9 @@
 // sampling_api.hip -- the C-ABI entry points (include/lmrs_sampling.h).
 //
-// Host-side argument checks, then one launch of one workgroup per row on the
-// caller's stream (the kernels live in their own translation units, behind
-// launch.hpp).  Nothing here allocates device memory.
+// Host-side argument checks, then one launch on the caller's stream (the
+// kernels live in their own translation units, behind launch.hpp): one
+// workgroup per row, or for the widest bf16 rows in batches of more rows than
+// CUs one persistent workgroup per CU.  Nothing here allocates device memory.
 #include "lmrs_sampling.h"
 #include "launch.hpp"
 
@@ -20,6 +21,20 @@ int check_args(const lmrs_sample_args *a, bool need_tokens) {
   const size_t esz = a->dtype == LMRS_DTYPE_BF16 ? 2 : 4;
   if (((uintptr_t)a->logits) % esz != 0) return LMRS_ERR_ALIGNMENT;
   return LMRS_OK;
+}
+
+// Workgroups of a persistent launch: one per CU of the current device
+// (queried once per device), at most one per row.
+int fast_grid(int batch) {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return batch < cus[dev] ? batch : cus[dev];
 }
 
 int vector_ok(const lmrs_sample_args *a) {
@@ -40,14 +55,15 @@ extern "C" int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream) {
   // not take finish in the generic engine, in the same launch)
   constexpr int64_t kSlot = lmrs::kFastSlotLogits;
   if (args->dtype == LMRS_DTYPE_BF16 && vec && V > 0 && V % 8 == 0 && V <= lmrs::kFastVocabMax) {
+    const int grid = fast_grid(args->batch);
     if (V <= 8 * kSlot)
-      lmrs::launch_fast_bf16_8(*args, s);
+      lmrs::launch_fast_bf16_8(*args, grid, s);
     else if (V <= 16 * kSlot)
-      lmrs::launch_fast_bf16_16(*args, s);
+      lmrs::launch_fast_bf16_16(*args, grid, s);
     else if (V <= 32 * kSlot)
-      lmrs::launch_fast_bf16_32(*args, s);
+      lmrs::launch_fast_bf16_32(*args, grid, s);
     else
-      lmrs::launch_fast_bf16_40(*args, s);
+      lmrs::launch_fast_bf16_40(*args, grid, s);
   } else if (args->dtype == LMRS_DTYPE_BF16) {
     lmrs::launch_generic_bf16(*args, vec, s);
   } else {

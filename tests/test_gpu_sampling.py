@@ -552,10 +552,14 @@ def test_randomized_rows_every_path():
     from 1 to beyond the window; top-p; min-p; histories), against the oracle."""
     W = _wl()
     rng = np.random.default_rng(2024)
-    for V, B in ((32000, 160), (128256, 96)):
+    # the last two cases have more rows than the GPU has CUs: rows in rounds
+    # (one workgroup per row, and for the widest rows persistent workgroups
+    # that take several rows each), NaN rows (the generic engine inside the
+    # same workgroup) among them
+    for V, B, kinds in ((32000, 160, 6), (128256, 96, 6), (8192, 700, 7), (140000, 320, 7)):
         rows, ks, ps, mps, ts, hists = [], [], [], [], [], []
         for _ in range(B):
-            kind = rng.integers(6)
+            kind = rng.integers(kinds)
             if kind == 0:
                 x = rng.normal(0, rng.uniform(0.3, 4.0), V)
             elif kind == 1:
@@ -567,8 +571,11 @@ def test_randomized_rows_every_path():
                 x[rng.choice(V, rng.integers(1, 20), replace=False)] += rng.uniform(5, 30)
             elif kind == 4:
                 x = rng.integers(-8, 8, V).astype(np.float64) / 2  # wide ties
-            else:
+            elif kind == 5:
                 x = rng.gumbel(0, 2.0, V)
+            else:
+                x = rng.normal(0, 1, V)
+                x[rng.integers(V)] = np.nan
             rows.append(x.astype(np.float32))
             ks.append(int(rng.choice([0, 0, -1, 1, 2, 10, 50, 64, 65, 300, 1000, 4096, 5000, V + 3])))
             ps.append(float(rng.choice([1.0, 1.0, rng.uniform(0.05, 1.0), 0.999])))
