@@ -58,7 +58,10 @@ extern "C" {
 #define LMRS_ROW_PARAM 3        /* a parameter fails its constructor's validation (repetition.rs:57-64,
                                    presence.rs:61-71, temperature.rs:43-50, top_p.rs:26-31,
                                    min_p.rs:27-29); top_k < -1 */
-#define LMRS_ROW_HISTORY 4      /* history longer than LMRS_MAX_HISTORY for this row */
+#define LMRS_ROW_HISTORY 4      /* more than LMRS_MAX_HISTORY_DISTINCT distinct history tokens in this row,
+                                   or one token more than LMRS_MAX_HISTORY_COUNT times (any length is
+                                   taken otherwise; repetition.rs:88-97 and presence.rs:107-117 have
+                                   no limit) */
 /* ... and flag bits above it. */
 #define LMRS_ROW_NEAR_BOUNDARY 0x100 /* the uniform lies within 1e-6 of a CDF boundary of the chosen
                                         token, or the nucleus cumulative lies within 1e-6 of top_p at
@@ -76,7 +79,8 @@ extern "C" {
 #define LMRS_GREEDY (-1)
 
 #define LMRS_MAX_VOCAB 262144  /* largest vocab accepted (2^18) */
-#define LMRS_MAX_HISTORY 4096  /* longest per-row history accepted */
+#define LMRS_MAX_HISTORY_DISTINCT 12288 /* distinct history tokens per row accepted */
+#define LMRS_MAX_HISTORY_COUNT 16383    /* occurrences of one history token accepted */
 
 typedef struct lmrs_sample_args {
   /* logits: device, `batch` rows of `row_stride` elements of `dtype`; only the

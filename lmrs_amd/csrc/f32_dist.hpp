@@ -443,7 +443,8 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
     dx.ctr[0] = NW;  // the batch counters of the two passes
     dx.ctr[1] = NW;
   }
-  if (c.hist_on) build_history<NT>(sh.ht, a, c, V);
+  // a history beyond the tables: the generic engine reports the row
+  if (c.hist_on && !build_history<NT>(sh.ht, a, c, V)) return false;
   uint32_t smax = 0u, smin = ~0u;
   {
     const float xs[4] = {sv.x, sv.y, sv.z, sv.w};
@@ -725,8 +726,9 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
 
   // ---- one wave resolves the row; the others wait at the barrier below ----
   if (threadIdx.x < 64u) {
-    uint64_t *const lst = (uint64_t *)sh.ht.keys;  // the history tables are no longer read
-    double *const wl = (double *)sh.ht.counts;
+    // the history tables are no longer read: their slots hold the two lists
+    uint64_t *const lst = (uint64_t *)sh.ht.slots;
+    double *const wl = (double *)(sh.ht.slots + kHashCap / 2);
     const uint64_t *const gat = ss.gather;
     const uint32_t fb1 = off1 << lsh, fb2 = off2 << lsh;
     // row cumulative = bucket cumulative + the range's offset, from a table

@@ -69,7 +69,8 @@ constexpr int kFastMaxVocab = kMaxSlots * 8 * kFT;
 constexpr int kMaxWords = kFastMaxVocab / 32;  // bitmap words
 constexpr int kWordsPer = kMaxWords / kFT;     // bitmap words per thread (rank map build)
 constexpr int kMaxWindow = kFT;     // widest window of the count cascade (one bin per thread)
-constexpr int kHistPer = LMRS_MAX_HISTORY / kFT;
+constexpr int kFastHistory = 4096;  // history ids a row of the fast path may have (longer: generic engine)
+constexpr int kHistPer = kFastHistory / kFT;
 constexpr int kMemPer = kFastMembers / kFT;
 constexpr int kSmallK = 64;         // top_k bound of the thread-value path
 constexpr int kTvBins = 256;        // bins of the thread-value histogram
@@ -281,7 +282,7 @@ constexpr int kLOffWbin = 64 * 1024;     // lean pass: exp(y - y0) of each candi
 constexpr int kFinishBins = 256;         // the bins stream_finish scans below the largest key
 static_assert(kLOffHash + kLHashSlots * 4 <= kLOffRecRaw && kLOffBinMin + kCandBins * 4 <= kOffCand, "lean views");
 static_assert(kOffMatch + kFW * kCandSeg * 4 <= kOffWhist, "candidate views");
-static_assert(LMRS_MAX_HISTORY * 2 <= kLHashSlots && kFastMaxVocab < (1 << 18) && LMRS_MAX_HISTORY < (1 << 14),
+static_assert(kFastHistory * 2 <= kLHashSlots && kFastMaxVocab < (1 << 18) && kFastHistory < (1 << 14),
               "hash load and packing");
 static_assert(kOffPrefix + kMaxWords * 2 <= kOffWhist, "prefix view");
 static_assert((int)sizeof(SelState) <= kOffWhist, "SelState view");
@@ -294,7 +295,7 @@ static_assert(kOffMembers + kFastMembers * 12 <= kArenaBytes, "member view");
 static_assert(kOffEntries + kMaxEntries * 4 <= kArenaBytes, "entries view");
 static_assert(kMaxEntries * 12 <= kOffEntries, "prefix view");
 static_assert(kOffTcnt + kFT * 4 <= kOffEntries, "ordered search view");
-static_assert(kFastMembers % kFT == 0 && LMRS_MAX_HISTORY % kFT == 0 && kMaxWords % kFT == 0, "per-thread counts");
+static_assert(kFastMembers % kFT == 0 && kFastHistory % kFT == 0 && kMaxWords % kFT == 0, "per-thread counts");
 
 struct FastShared {
   alignas(16) unsigned char arena[kArenaBytes];
@@ -1736,7 +1737,10 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
 #pragma unroll
   for (int s = 0; s < kPre; ++s) kv[s] = issue_slot(s);
   const RowCfg c = uniform_cfg(load_row_cfg(a, r, LMRS_DTYPE_BF16));
-  const bool hist = c.status == LMRS_ROW_OK && c.hist_on;
+  // a history longer than the registers hold goes to the generic engine
+  // (after the load pass, which every row completes)
+  const bool long_hist = c.status == LMRS_ROW_OK && c.hist_on && c.h_len > kFastHistory;
+  const bool hist = c.status == LMRS_ROW_OK && c.hist_on && !long_hist;
   uint32_t hid[kHistPer];
   issue_history_ids(hid, a, c, hist, rowp);
   const bool k_on = c.top_k > 0 && c.top_k < V;
@@ -1744,8 +1748,8 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   // pass; one that declines is read again by the general pass, in the same
   // order of requests.
   // (not in the widest instantiation: its registers would spill)
-  const bool lean = NCH <= 32 && c.status == LMRS_ROW_OK && (c.greedy || (k_on && c.top_k <= kSmallK)) &&
-                    penalties_lower(c);
+  const bool lean = NCH <= 32 && c.status == LMRS_ROW_OK && !long_hist &&
+                    (c.greedy || (k_on && c.top_k <= kSmallK)) && penalties_lower(c);
   if constexpr (NCH <= 32) {
     if (lean) {
       if (lean_row<NCH, kPre>(sh, a, r, c, kv, hid, hist, src, nchunks)) return true;
@@ -1836,7 +1840,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     if (tid == 0) write_row(a, r, 0u, 0.0f, 0.0f, c.status);
     return true;
   }
-  if (hist && !mem_ok) return false;
+  if (long_hist || (hist && !mem_ok)) return false;
   // The thread value: the largest chunk maximum when that chunk holds no
   // member (else none), raised to the members' z keys -- each a distinct
   // element's key.

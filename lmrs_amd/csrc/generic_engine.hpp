@@ -626,7 +626,10 @@ __device__ __forceinline__ void generic_row(GenericShared &sh, const lmrs_sample
       write_row(a, r, 0u, 0.0f, 0.0f, c.status != LMRS_ROW_OK ? c.status : LMRS_ROW_EMPTY);
     return;
   }
-  if (c.hist_on) build_history<NT>(sh.ht, a, c, V);
+  if (c.hist_on && !build_history<NT>(sh.ht, a, c, V)) {  // the history exceeds the tables
+    if (threadIdx.x == 0) write_row(a, r, 0u, 0.0f, 0.0f, LMRS_ROW_HISTORY);
+    return;
+  }
   StreamRow<DT, NT> row;
   row.base = (const char *)a.logits + (size_t)r * (size_t)a.row_stride * TR::kElemBytes;
   row.vocab = V;
@@ -658,8 +661,11 @@ __global__ void __launch_bounds__(kThreads) process_kernel(lmrs_sample_args a, v
   if (c.status != LMRS_ROW_OK) {  // invalid rows are copied unchanged
     c.hist_on = c.rep_on = c.pres_on = c.temp_on = 0;
   }
+  if (c.hist_on && !build_history(ht, a, c, V)) {  // the history exceeds the tables: copied unchanged
+    c.status = LMRS_ROW_HISTORY;
+    c.hist_on = c.rep_on = c.pres_on = c.temp_on = 0;
+  }
   if (threadIdx.x == 0 && a.status) a.status[r] = c.status;
-  if (c.hist_on) build_history(ht, a, c, V);
   const char *src = (const char *)a.logits + (size_t)r * (size_t)a.row_stride * TR::kElemBytes;
   char *dst = (char *)out + (size_t)r * (size_t)V * TR::kElemBytes;
   for (int64_t i = threadIdx.x; i < V; i += kThreads) {

@@ -13,11 +13,6 @@
 
 namespace lmrs {
 
-constexpr int kHashCap = 2 * LMRS_MAX_HISTORY;  // open addressing, load <= 1/2
-constexpr int kHashBits = 13;
-static_assert((1 << kHashBits) == kHashCap, "hash size");
-constexpr int kBitmapWords = LMRS_MAX_VOCAB / 32;
-
 struct RowCfg {
   int status;          // LMRS_ROW_OK or an error code decided before sampling
   int rep_on, pres_on, temp_on, hist_on;
@@ -32,12 +27,24 @@ struct RowCfg {
   int64_t h_begin, h_len;
 };
 
-// History tables in LDS: a membership bitmap over the vocab and a hash map
-// token -> multiplicity (the HashMap of presence.rs:107-110).
+// History tables of the generic and f32 engines: the vocab's membership
+// bitmap and a hash map token -> multiplicity (the HashMap of
+// presence.rs:107-110), one 32-bit slot per token: token | count << 18
+// (0 = empty; an occupied slot counts at least 1).  Any history length is
+// taken; a row with more than LMRS_MAX_HISTORY_DISTINCT distinct tokens (the
+// table would pass 3/4 full) or a token more than LMRS_MAX_HISTORY_COUNT
+// times (the count field) gets LMRS_ROW_HISTORY.
+constexpr int kHashBits = 14;
+constexpr int kHashCap = 1 << kHashBits;
+constexpr int kBitmapWords = LMRS_MAX_VOCAB / 32;
+constexpr uint32_t kSlotTokenMask = (1u << 18) - 1u;
+static_assert(LMRS_MAX_VOCAB <= (1 << 18) && LMRS_MAX_HISTORY_COUNT == (1 << 14) - 1 &&
+              LMRS_MAX_HISTORY_DISTINCT * 4 <= kHashCap * 3, "slot packing and load");
+
 struct HistoryTables {
-  uint32_t keys[kHashCap];   // token + 1, 0 = empty
-  uint32_t counts[kHashCap];
+  uint32_t slots[kHashCap];
   uint32_t bitmap[kBitmapWords];
+  uint32_t distinct, overflow;
 };
 
 __device__ __forceinline__ uint32_t hash_slot(uint32_t t) {
@@ -46,12 +53,13 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t t) {
 
 __device__ __forceinline__ uint32_t history_count(const HistoryTables &ht, uint32_t t) {
   uint32_t s = hash_slot(t);
-  for (;;) {  // terminates: the table is at most half full
-    uint32_t k = ht.keys[s];
-    if (k == t + 1u) return ht.counts[s];
-    if (k == 0u) return 0u;
+  for (uint32_t n = 0; n < (uint32_t)kHashCap; ++n) {  // ends: the table is at most 3/4 full
+    const uint32_t v = ht.slots[s];
+    if (v == 0u) return 0u;
+    if ((v & kSlotTokenMask) == t) return v >> 18;
     s = (s + 1u) & (kHashCap - 1);
   }
+  return 0u;
 }
 
 __device__ __forceinline__ bool history_member(const HistoryTables &ht, uint32_t i) {
@@ -125,7 +133,6 @@ __device__ inline RowCfg load_row_cfg(const lmrs_sample_args &a, int r, int dtyp
   c.h_begin = h0;
   c.h_len = h1 - h0;
   if (c.h_len < 0) c.status = LMRS_ROW_PARAM;
-  if (c.h_len > LMRS_MAX_HISTORY && c.status == LMRS_ROW_OK) c.status = LMRS_ROW_HISTORY;
   const bool has_hist = c.h_len > 0;
   c.rep_on = (rep != 1.0f) && has_hist;                        // repetition.rs:82-84
   c.pres_on = has_hist && !(pres == 0.0f && freq == 0.0f);     // presence.rs:102-104
@@ -187,30 +194,49 @@ __device__ __forceinline__ uint32_t minp_low_key(uint32_t lo, uint32_t hi, doubl
 
 // Builds the history tables for the row (all NT threads; ends with a barrier).
 template <int NT = kThreads>
-__device__ inline void build_history(HistoryTables &ht, const lmrs_sample_args &a,
+__device__ inline bool build_history(HistoryTables &ht, const lmrs_sample_args &a,
                                      const RowCfg &c, int64_t vocab) {
-  for (int i = threadIdx.x; i < kHashCap; i += NT) {
-    ht.keys[i] = 0u;
-    ht.counts[i] = 0u;
-  }
+  for (int i = threadIdx.x; i < kHashCap; i += NT) ht.slots[i] = 0u;
   const int words = (int)((vocab + 31) >> 5);
   for (int i = threadIdx.x; i < words; i += NT) ht.bitmap[i] = 0u;
+  if (threadIdx.x == 0) {
+    ht.distinct = 0u;
+    ht.overflow = 0u;
+  }
   __syncthreads();
   for (int64_t j = threadIdx.x; j < c.h_len; j += NT) {
-    uint32_t t = a.hist_ids[c.h_begin + j];
+    const uint32_t t = a.hist_ids[c.h_begin + j];
     if ((int64_t)t >= vocab) continue;  // ids outside the vocab are ignored
     atomicOr(&ht.bitmap[t >> 5], 1u << (t & 31u));
     uint32_t s = hash_slot(t);
-    for (;;) {
-      uint32_t prev = atomicCAS(&ht.keys[s], 0u, t + 1u);
-      if (prev == 0u || prev == t + 1u) {
-        atomicAdd(&ht.counts[s], 1u);
+    for (uint32_t n = 0;; ++n, s = (s + 1u) & (kHashCap - 1)) {
+      if (n == (uint32_t)kHashCap) {  // full (only after the distinct limit has been passed)
+        ht.overflow = 1u;
         break;
       }
-      s = (s + 1u) & (kHashCap - 1);
+      const uint32_t prev = atomicCAS(&ht.slots[s], 0u, t | (1u << 18));
+      if (prev == 0u) {
+        if (atomicAdd(&ht.distinct, 1u) >= (uint32_t)LMRS_MAX_HISTORY_DISTINCT) ht.overflow = 1u;
+        break;
+      }
+      if ((prev & kSlotTokenMask) == t) {
+        // a count about to leave its 14 bits is not added (the row is reported)
+        uint32_t cur = prev;
+        for (;;) {
+          if ((cur >> 18) >= (uint32_t)LMRS_MAX_HISTORY_COUNT) {
+            ht.overflow = 1u;
+            break;
+          }
+          const uint32_t seen = atomicCAS(&ht.slots[s], cur, cur + (1u << 18));
+          if (seen == cur) break;
+          cur = seen;
+        }
+        break;
+      }
     }
   }
   __syncthreads();
+  return ht.overflow == 0u;
 }
 
 // The processor chain on one bf16 element (16-bit pattern in, out).

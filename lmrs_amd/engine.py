@@ -104,7 +104,7 @@ class SequenceState:
 
 _ROW_MESSAGES = {S.ROW_EMPTY: "cannot sample from empty logits",
                  S.ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
-                 S.ROW_PARAM: "invalid sampling parameter", S.ROW_HISTORY: "history too long"}
+                 S.ROW_PARAM: "invalid sampling parameter", S.ROW_HISTORY: "history beyond the sampler's tables"}
 
 
 class BatchSamplingError(S.SamplingError):

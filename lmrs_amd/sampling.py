@@ -27,7 +27,8 @@ ROW_OK, ROW_EMPTY, ROW_DISTRIBUTION, ROW_PARAM, ROW_HISTORY = 0, 1, 2, 3, 4
 ROW_NEAR_BOUNDARY = 0x100
 GREEDY = -1  # top_k value selecting Greedy (greedy.rs:22-29); top_k = 1 is TopK(1)
 MAX_VOCAB = 262144
-MAX_HISTORY = 4096
+MAX_HISTORY_DISTINCT = 12288  # distinct history tokens per row (LMRS_MAX_HISTORY_DISTINCT)
+MAX_HISTORY_COUNT = 16383     # occurrences of one history token (LMRS_MAX_HISTORY_COUNT)
 
 
 class SampleArgs(ctypes.Structure):
@@ -440,6 +441,6 @@ class Sampler:
                 raise SamplingError({ROW_EMPTY: "cannot sample from empty logits",
                                      ROW_DISTRIBUTION: "logits produced an invalid probability distribution",
                                      ROW_PARAM: "invalid sampling parameter",
-                                     ROW_HISTORY: "history too long"}.get(int(st[j]), f"status {int(st[j])}"))
+                                     ROW_HISTORY: "history beyond the sampler's tables"}.get(int(st[j]), f"status {int(st[j])}"))
             out.append(SampleOutput(int(tok[j]) & 0xFFFFFFFF, float(lp[j]), float(lg[j])))
         return out

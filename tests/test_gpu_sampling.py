@@ -87,7 +87,7 @@ def test_processors_exhaustive_bf16():
     allb = np.arange(V, dtype=np.uint32).astype(np.uint16)
     configs = [(1.1, 0.5, 0.3, 0.7), (2.0, 0.0, 0.0, 1.0), (0.7, -1.0, 0.125, 1.5), (1.0, 0.5, 0.25, 1e-3),
                (1.05, 0.0, 0.7, 3.0)]
-    # each config runs on 32 rows whose histories (<= LMRS_MAX_HISTORY ids each)
+    # each config runs on 32 rows whose histories (<= 4096 ids each)
     # together mark every pattern once, twice (counts 2) or not at all
     reps = 32
     rows = [(c, o) for c in configs for o in range(reps)]
@@ -299,22 +299,43 @@ def test_special_values_and_statuses():
 
 
 def test_history_limits_and_out_of_range_ids():
+    """Histories of any length (repetition.rs:88-97 and presence.rs:107-117 have
+    no limit): out-of-range ids are ignored; 4096 ids (the fast kernel's
+    registers) and 4097 (the generic engine); 20000 ids with about ten
+    thousand distinct tokens, and 50000 ids with heavy repeats, through
+    the fast kernel's rows (bf16, V % 8 == 0), the generic bf16 engine (odd V)
+    and f32 rows; the two table limits report LMRS_ROW_HISTORY."""
     from lmrs_amd import sampling as S
 
     W = _wl()
     rng = np.random.default_rng(14)
-    V = 5000
-    x = W.f32_to_bf16_bits((rng.standard_normal((3, V)) * 2).astype(np.float32))
-    hist = [list(rng.integers(0, V, 100)) + [V, V + 1, 2**32 - 1],   # out-of-range ids ignored
-            list(rng.integers(0, V, S.MAX_HISTORY)),                 # at the limit
-            list(rng.integers(0, V, S.MAX_HISTORY + 1))]             # over the limit
-    w = _mk(x, history=hist, rep=[1.3] * 3, pres=[0.4] * 3, freq=[0.2] * 3, t=[0.9] * 3, k=[40] * 3,
-            p=[0.9] * 3, u=[0.3, 0.6, 0.9])
-    g = run_gpu(w)
-    assert (g["status"][2] & 0xFF) == S.ROW_HISTORY
-    r = run_oracle(w.rows([0, 1]))
-    sub = {k: v[:2] for k, v in g.items()}
-    assert_parity(compare(sub, r), "history")
+    for V in (128256, 128255):
+        # 20000 ids: 9000 distinct tokens once each, then 11000 Zipf(1.1) draws
+        zipf = rng.permutation(V)[:9000].tolist() + W._zipf_history(rng, 1, 11000, V)[1].tolist()
+        rng.shuffle(zipf)
+        assert 9000 < len(set(zipf)) <= S.MAX_HISTORY_DISTINCT
+        heavy = list(rng.integers(0, 64, 50000))  # 64 tokens, each ~780 times
+        hist = [list(rng.integers(0, V, 100)) + [V, V + 1, 2**32 - 1],   # out-of-range ids ignored
+                list(rng.integers(0, V, 4096)),
+                list(rng.integers(0, V, 4097)),
+                zipf, heavy,
+                list(rng.permutation(V)[:S.MAX_HISTORY_DISTINCT + 1]),     # too many distinct tokens
+                [7] * (S.MAX_HISTORY_COUNT + 1)]                           # one token too often
+        B = len(hist)
+        for dt in ("bf16", "f32"):
+            x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+            xx = W.f32_to_bf16_bits(x) if dt == "bf16" else x
+            w = _mk(xx, history=hist, rep=[1.3] * B, pres=[0.4] * B, freq=[0.2] * B, t=[0.9] * B,
+                    k=[0, 40, 0, 0, 50, 40, 40], p=[0.9] * B, u=rng.random(B))
+            print(f"[case] histories {dt} V={V} lengths {[len(h) for h in hist]}", flush=True)
+            g = run_gpu(w)
+            assert list(g["status"][-2:] & 0xFF) == [S.ROW_HISTORY] * 2, g["status"]
+            ok = list(range(B - 2))
+            r = run_oracle(w.rows(ok))
+            sub = {k: v[:B - 2] for k, v in g.items()}
+            rep = compare(sub, r)
+            _report(f"history-{dt}-{V}", rep)
+            assert_parity(rep, f"history-{dt}-{V}")
 
 
 def test_uniform_extremes():
