@@ -184,6 +184,46 @@ def copy_calibration(size_mb: int, reps: int) -> None:
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "reps": reps}), flush=True)
 
 
+def lm_head_bench(steps: int, warmup: int) -> dict:
+    """Times lmrs_lm_head_fwd (the LM head's projection with the sampling
+    prologue in its epilogue) at C3's rows and vocab with a 4096-wide hidden
+    state: 256 x 4096 x 128256, two weight matrices in rotation (2.1 GB, over
+    the MALL).  Reported beside the metric, never as it."""
+    import torch
+
+    from lmrs_amd import sampling as S
+
+    rows, K, V = 256, 4096, 128256
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(rows, K, device=dev, generator=g).to(torch.bfloat16)
+    ws = [(torch.randn(V, K, device=dev, generator=g) * (2.5 / K ** 0.5)).to(torch.bfloat16) for _ in range(2)]
+    s = torch.cuda.Stream(device=dev)
+    res = {}
+    for fused in (True, False):
+        with torch.cuda.stream(s):
+            for i in range(warmup):
+                S.lm_head(x, ws[i % 2], tile_max=fused, stream=s)
+            s.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for i in range(steps):
+                S.lm_head(x, ws[i % 2], tile_max=fused, stream=s)
+            e1.record(s)
+            e1.synchronize()
+        res["fused" if fused else "plain"] = e0.elapsed_time(e1) / steps * 1e3
+    us = res["fused"]
+    flops = 2.0 * rows * K * V
+    nbytes = V * K * 2 + rows * K * 2 + rows * V * 2 + rows * ((V + 63) // 64) * 8
+    log(f"bench: lm_head {rows}x{K}x{V}: {us:.1f} us with the tile maxima, {res['plain']:.1f} us without")
+    return {"kernel": "lm_head_kernel (lmrs_lm_head_fwd)", "shape": [rows, K, V], "us": us,
+            "us_without_tile_max": res["plain"],
+            "mfma": {"achieved": flops / (us * 1e-6) / 1e12, "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": flops / (us * 1e-6) / 1e12 / 2500.0},
+            "hbm": {"achieved": nbytes / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -195,6 +235,9 @@ def main() -> int:
                          "generic bf16 kernel); a parity and counter case, not the metric")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--lm-head", action="store_true",
+                    help="also time the LM head's projection with the fused sampling prologue "
+                         "(256 x 4096 x 128256 bf16); reported as 'lm_head', not as the metric")
     ap.add_argument("--copy-calibration", type=int, metavar="MB", default=0,
                     help="run only a device copy of MB megabytes (counter calibration)")
     args = ap.parse_args()
@@ -317,6 +360,8 @@ def main() -> int:
                            "kernel": "lmrs_stream_probe (the load pass alone, same access shape)",
                            "frac": (alg / (ms * 1e-3) / 1e9) / ceiling if ceiling else None},
     }
+    if args.lm_head:
+        line["lm_head"] = lm_head_bench(max(5, args.steps // 10), 3)
     if not args.no_cpu:
         log("bench: CPU baseline (oracle) ...")
         line["cpu_baseline"], line["parity_sample"] = cpu_baseline(w, res, args.cpu_seconds)

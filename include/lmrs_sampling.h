@@ -145,6 +145,25 @@ int lmrs_sample_fwd(const lmrs_sample_args *args, void *stream);
  * min_p, uniforms and the other outputs are neither read nor checked. */
 int lmrs_process_logits_fwd(const lmrs_sample_args *args, void *out, void *stream);
 
+/* The LM head's vocabulary projection with the sampling prologue in its
+ * epilogue: out[r, v] = bf16(sum_k input[r, k] * weight[v, k]) for `rows`
+ * rows of `in_features` bf16 hidden values and a [out_features, in_features]
+ * bf16 weight (row-major, out [rows, out_features] contiguous), f32
+ * accumulation on the matrix cores.  Replaces, for the LM head (bf16, no
+ * bias), LmHead::forward (crates/ops/src/embedding/lm_head.rs:33-35) ->
+ * kernels::linear -> linear_fwd (kernels/ffi/tensor_ffi.cu:820-841,
+ * linear_kernel :230-258), whose argument order it keeps; the sums run in
+ * the matrix unit's order, so a logit may differ from linear_kernel's by the
+ * rounding of its f32 sum.  When tile_max is not NULL it receives, for every
+ * row r and 64-column tile t, the tile's largest logit in the sampler's total
+ * order: tile_max[r * ceil(out_features / 64) + t] = key << 32 | ~column,
+ * key the 16-bit order key of the bf16 pattern (negatives flipped, sign bit
+ * set on non-negatives), ties to the lower column.  dtype must be
+ * LMRS_DTYPE_BF16; in_features % 8 == 0; input and weight 16-byte aligned.
+ * Asynchronous on `stream`; allocates nothing. */
+int lmrs_lm_head_fwd(void *out, const void *input, const void *weight, int32_t rows, int32_t in_features,
+                     int32_t out_features, int32_t dtype, uint64_t *tile_max, void *stream);
+
 /* Device workspace, in bytes, that lmrs_sample_fwd needs for a call of this
  * shape: always 0.  Every working set (history tables, candidate lists,
  * histograms) lives in the workgroup's LDS and registers, so the caller

@@ -77,6 +77,10 @@ def lib():
         L.lmrs_process_logits_fwd.restype = ctypes.c_int
         L.lmrs_sample_workspace_size.argtypes = [ctypes.c_int32, ctypes.c_int64, ctypes.c_int32, ctypes.c_int64]
         L.lmrs_sample_workspace_size.restype = ctypes.c_size_t
+        L.lmrs_lm_head_fwd.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32,
+                                       ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+        L.lmrs_lm_head_fwd.restype = ctypes.c_int
         L.lmrs_sampling_version.argtypes = []
         L.lmrs_sampling_version.restype = ctypes.c_char_p
         _lib = L
@@ -245,6 +249,37 @@ def process_logits(logits, *, hist_offsets=None, hist_ids=None, repetition_penal
         raise SamplingError(f"lmrs_process_logits_fwd failed with code {rc}")
     torch.cuda.current_stream(dev).synchronize() if stream is None else None
     return out, status
+
+
+LM_HEAD_TILE = 64  # columns per tile_max entry of lmrs_lm_head_fwd
+
+
+def lm_head(hidden, weight, *, tile_max: bool = True, stream=None):
+    """LmHead::forward (crates/ops/src/embedding/lm_head.rs:33-35) on the matrix
+    cores: logits [rows, V] bf16 = hidden [rows, H] bf16 @ weight[V, H]^T, and
+    (tile_max) the sampling prologue of the epilogue, int64 [rows, ceil(V/64)]
+    holding key << 32 | ~column of each 64-column tile's largest logit.
+    Asynchronous on `stream` (default: the current stream)."""
+    torch = _torch()
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("hidden must be [rows, H] and weight [V, H]")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("lm_head takes bf16 hidden states and weights")
+    hidden, weight = hidden.contiguous(), weight.contiguous()
+    rows, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    out = torch.empty((rows, V), dtype=torch.bfloat16, device=dev)
+    tm = torch.empty((rows, (V + LM_HEAD_TILE - 1) // LM_HEAD_TILE), dtype=torch.int64, device=dev) if tile_max else None
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    _on_stream(s, [hidden, weight, out, tm])
+    rc = lib().lmrs_lm_head_fwd(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(hidden.data_ptr()),
+                                ctypes.c_void_p(weight.data_ptr()), rows, H, V, DTYPE_BF16,
+                                ctypes.c_void_p(tm.data_ptr()) if tm is not None else None,
+                                ctypes.c_void_p(s.cuda_stream))
+    if rc != LMRS_OK:
+        raise SamplingError(f"lmrs_lm_head_fwd failed with code {rc}")
+    return out, tm
 
 
 # ---------------------------------------------------------------------------

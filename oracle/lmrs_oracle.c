@@ -522,3 +522,22 @@ int lmrs_oracle_sample_batch(const void *logits, int dtype, int64_t batch, int64
   free(th);
   return LMRS_ORACLE_OK;
 }
+
+/* linear_kernel (kernels/ffi/tensor_ffi.cu:230-258), bf16, no bias. */
+void lmrs_oracle_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t in, int64_t out,
+                             uint16_t *y, float *acc_out, double *sum_abs) {
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t v = 0; v < out; ++v) {
+      float acc = 0.0f;
+      double sa = 0.0;
+      for (int64_t k = 0; k < in; ++k) {
+        const float p = lmrs_oracle_f32_from_bf16(x[r * in + k]) * lmrs_oracle_f32_from_bf16(w[v * in + k]);
+        acc += p;
+        sa += fabs((double)p);
+      }
+      y[r * out + v] = lmrs_oracle_bf16_from_f32_dev(acc);
+      if (acc_out) acc_out[r * out + v] = acc;
+      if (sum_abs) sum_abs[r * out + v] = sa;
+    }
+  }
+}

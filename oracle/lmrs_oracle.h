@@ -147,6 +147,17 @@ int lmrs_oracle_sample_batch(const void *logits, int dtype, int64_t batch, int64
                              const double *uniforms, lmrs_oracle_output *out,
                              lmrs_oracle_diag *diag, int32_t *status, int n_threads);
 
+/* ---- the LM head's projection ---------------------------------------------
+ * linear_kernel (kernels/ffi/tensor_ffi.cu:230-258) for bf16 without bias, as
+ * LmHead::forward calls it (crates/ops/src/embedding/lm_head.rs:33-35):
+ * y[r, v] = bf16(acc), acc = 0.0f then acc += f32(x[r, k]) * f32(w[v, k]) for
+ * k = 0 .. in-1 in order (each product of two bf16 is exact in f32, so nvcc's
+ * contraction to an fma rounds the same), bf16 round to nearest even
+ * (from_float, activation_kernels.cuh:35-38).  Also returns, when sum_abs is
+ * not NULL, sum_k |x w| per output (for error bounds). */
+void lmrs_oracle_linear_bf16(const uint16_t *x, const uint16_t *w, int64_t rows, int64_t in, int64_t out,
+                             uint16_t *y, float *acc_out, double *sum_abs);
+
 #ifdef __cplusplus
 }
 #endif

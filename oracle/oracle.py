@@ -88,8 +88,25 @@ def lib():
                                              outp, ctypes.POINTER(Diag), P]
         L.lmrs_oracle_sample_batch.argtypes = [P, ctypes.c_int, i64, i64, i64, P, P, P, P, P, P, P,
                                                ctypes.c_int]
+        L.lmrs_oracle_linear_bf16.argtypes = [P, P, i64, i64, i64, P, P, P]
+        L.lmrs_oracle_linear_bf16.restype = None
         _lib = L
     return _lib
+
+
+def linear_bf16(x_bits: np.ndarray, w_bits: np.ndarray):
+    """linear_kernel (tensor_ffi.cu:230-258) for bf16 without bias: returns
+    (y bf16 bits [rows, out], f32 sums [rows, out], sum |x w| [rows, out])."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(w_bits, dtype=np.uint16)
+    rows, n_in = x.shape
+    n_out = w.shape[0]
+    assert w.shape[1] == n_in
+    y = np.empty((rows, n_out), dtype=np.uint16)
+    acc = np.empty((rows, n_out), dtype=np.float32)
+    sa = np.empty((rows, n_out), dtype=np.float64)
+    lib().lmrs_oracle_linear_bf16(_ptr(x), _ptr(w), rows, n_in, n_out, _ptr(y), _ptr(acc), _ptr(sa))
+    return y, acc, sa
 
 
 def _ptr(a):

@@ -135,3 +135,19 @@ def test_python_next_unit_matches_oracle():
 
     for seed in (1, 9, 42, 2**64 - 1):
         assert S.next_unit(seed) == O.next_unit(seed)
+
+
+@pytest.mark.parametrize(
+    "args,code",
+    [
+        ((0x1000, 0x2000, 0x3000, 4, 64, 100, S.DTYPE_F32, None, None), S.ERR_BAD_DTYPE),
+        ((0x1000, 0x2000, 0x3000, -1, 64, 100, S.DTYPE_BF16, None, None), S.ERR_BAD_SHAPE),
+        ((0x1000, 0x2000, 0x3000, 4, 60, 100, S.DTYPE_BF16, None, None), S.ERR_BAD_SHAPE),  # in % 8
+        ((None, 0x2000, 0x3000, 4, 64, 100, S.DTYPE_BF16, None, None), S.ERR_NULL_ARGUMENT),
+        ((0x1000, None, 0x3000, 4, 64, 100, S.DTYPE_BF16, None, None), S.ERR_NULL_ARGUMENT),
+        ((0x1000, 0x2008, 0x3000, 4, 64, 100, S.DTYPE_BF16, None, None), S.ERR_ALIGNMENT),
+        ((0x1000, 0x2000, 0x3000, 0, 64, 100, S.DTYPE_BF16, None, None), S.LMRS_OK),  # nothing to do
+    ],
+)
+def test_lm_head_host_side_rejection(args, code):
+    assert S.lib().lmrs_lm_head_fwd(*args) == code

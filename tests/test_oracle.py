@@ -553,3 +553,49 @@ def test_top_k_one_is_not_greedy_on_non_finite_rows():
     a = O.sample_row(x, None, O.make_params(top_k=1), 0.7)
     b = O.sample_row(x, None, O.make_params(top_k=O.GREEDY), 0.7)
     assert a[0] == b[0] == O.OK and a[1] == b[1] and a[1][0] == 1 and a[1][1] == 0.0
+
+
+# ---------------------------------------------------------------------------
+# the LM head's projection (linear_kernel, tensor_ffi.cu:230-258)
+# ---------------------------------------------------------------------------
+
+def test_linear_oracle_identity_and_one_hot():
+    """With w = I every output is one exact product: y = x.  With one-hot x
+    rows, y[r] picks a column of w."""
+    import oracle as O
+    from lmrs_amd import workloads as W
+
+    rng = np.random.default_rng(3)
+    n = 40
+    x = W.f32_to_bf16_bits(rng.normal(0, 3, (5, n)).astype(np.float32))
+    eye = W.f32_to_bf16_bits(np.eye(n, dtype=np.float32))
+    y, _, _ = O.linear_bf16(x, eye)
+    assert np.array_equal(y, x)
+    w = W.f32_to_bf16_bits(rng.normal(0, 1, (7, n)).astype(np.float32))
+    oh = np.zeros((3, n), np.float32)
+    oh[0, 4] = oh[1, 0] = oh[2, n - 1] = 1.0
+    y2, _, _ = O.linear_bf16(W.f32_to_bf16_bits(oh), w)
+    assert np.array_equal(y2, w[:, [4, 0, n - 1]].T)
+
+
+def test_linear_oracle_sums_in_order():
+    """The f32 sum is the sequential one of linear_kernel (acc += x * w over k):
+    numpy's float32 accumulate runs the same order; the bf16 output is its
+    round to nearest even; sum |x w| against float64."""
+    import oracle as O
+    from lmrs_amd import workloads as W
+
+    rng = np.random.default_rng(4)
+    rows, n_in, n_out = 6, 333, 29
+    xb = W.f32_to_bf16_bits(rng.normal(0, 2, (rows, n_in)).astype(np.float32))
+    wb = W.f32_to_bf16_bits(rng.normal(0, 0.05, (n_out, n_in)).astype(np.float32))
+    y, acc, sa = O.linear_bf16(xb, wb)
+    xf, wf = W.bf16_bits_to_f32(xb), W.bf16_bits_to_f32(wb)
+    prod = xf[:, None, :] * wf[None, :, :]  # exact in f32 (two 8-bit mantissas)
+    seq = np.add.accumulate(prod, axis=2, dtype=np.float32)[:, :, -1]
+    assert np.array_equal(acc.view(np.uint32), seq.view(np.uint32))
+    assert np.array_equal(y, W.f32_to_bf16_bits(seq))
+    assert np.allclose(sa, np.abs(prod.astype(np.float64)).sum(axis=2), rtol=1e-12)
+    # a different summation order moves the f32 sum by at most n * 2^-24 * sum |x w|
+    alt = prod.astype(np.float64).sum(axis=2)
+    assert np.all(np.abs(acc - alt) <= n_in * 2.0 ** -24 * sa)
