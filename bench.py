@@ -56,6 +56,8 @@ def kernel_label(w) -> str:
     """The kernel lmrs_sample_fwd launches for this workload (its dispatch rule)."""
     if w.dtype == "bf16" and w.vocab % 8 == 0 and 0 < w.vocab <= 40 * 4096:
         nch = next(n for n in (8, 16, 32, 40) if w.vocab <= n * 4096)
+        if nch == 40 and w.batch > 256:  # more rows than MI355X's CUs: the persistent launch
+            return f"bf16_fast_rounds_kernel<{nch}> (one launch per step)"
         return f"bf16_fast_kernel<{nch}> (one launch per step)"
     if w.dtype == "bf16":
         return "generic_sample_kernel<0> (one launch per step)"
