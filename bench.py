@@ -226,6 +226,36 @@ def lm_head_bench(steps: int, warmup: int) -> dict:
                     "frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bytes": nbytes}}
 
 
+def decode_bench(logits, steps: int) -> dict:
+    """Times the engine's decode step end to end (lmrs_amd.engine.DecodeBatch.step:
+    uniforms from each sequence's LCG, the launch, the outputs back on the
+    host, the tokens appended to the device-resident histories) over 256
+    sequences sampling from the workload's logits with T = 0.7 and top-k 50
+    (the engine maps a request to one strategy, generation.rs:352-365).
+    Reports the host wall time per step."""
+    import statistics
+
+    import torch
+
+    from lmrs_amd import engine as E
+
+    n = logits.shape[0]
+    cfg = E.GenerationConfig(max_tokens=steps + 10, temperature=0.7, top_p=1.0, top_k=50)
+    seqs = [E.SequenceState(cfg, seed=1 + i) for i in range(n)]
+    batch = E.DecodeBatch(seqs)
+    for _ in range(steps):
+        batch.step(logits)
+    torch.cuda.synchronize()
+    t = sorted(batch.timings[3:]) or batch.timings
+    med = statistics.median(t) * 1e6
+    log(f"bench: decode step (DecodeBatch.step, {n} sequences, host wall) median {med:.1f} us")
+    return {"sequences": n, "steps": len(batch.timings), "host_us_median": med,
+            "host_us_p10": t[int(0.1 * (len(t) - 1))] * 1e6, "host_us_p90": t[int(0.9 * (len(t) - 1))] * 1e6,
+            "history_len_at_end": len(seqs[0].generated),
+            "what": "DecodeBatch.step wall time on the host: uniforms, one launch, one copy of the four "
+                    "outputs back, in-place appends to the device histories"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -237,6 +267,9 @@ def main() -> int:
                          "generic bf16 kernel); a parity and counter case, not the metric")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--decode", type=int, metavar="STEPS", default=0,
+                    help="also time the engine's decode step end to end (host wall) over STEPS steps "
+                         "on the workload's logits; reported as 'decode_step'")
     ap.add_argument("--lm-head", action="store_true",
                     help="also time the LM head's projection with the fused sampling prologue "
                          "(256 x 4096 x 128256 bf16); reported as 'lm_head', not as the metric")
@@ -364,6 +397,8 @@ def main() -> int:
     }
     if args.lm_head:
         line["lm_head"] = lm_head_bench(max(5, args.steps // 10), 3)
+    if args.decode:
+        line["decode_step"] = decode_bench(bufs[0], args.decode)
     if not args.no_cpu:
         log("bench: CPU baseline (oracle) ...")
         line["cpu_baseline"], line["parity_sample"] = cpu_baseline(w, res, args.cpu_seconds)

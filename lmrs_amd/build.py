@@ -16,7 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liblmrs_sampling.so")
 
 # one translation unit per kernel family, compiled in parallel, then linked
-SOURCES = ["sampling_api.hip", "fast_nch8.hip", "fast_nch16.hip", "fast_nch32.hip", "fast_nch40.hip",
+SOURCES = ["fast_nch40_pairs.hip", "sampling_api.hip", "fast_nch8.hip", "fast_nch16.hip", "fast_nch32.hip",
+           "fast_nch40.hip",
            "generic_kernels.hip", "f32_kernel.hip", "lm_head.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -2287,29 +2287,36 @@ __global__ void __launch_bounds__(kFT) bf16_fast_kernel(lmrs_sample_args a) {
   generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, a, r, 1);
 }
 
-// A persistent launch for batches of more rows than CUs: gridDim.x
-// workgroups (one per CU) take the rows in rounds (round_row); every
-// workgroup leaves after its last row, and every wave of it runs the same
-// barriers per row.  MI355X's in-order dispatch of one workgroup per row
-// left CUs idle for up to 46 us between rows when another XCD had no CU
-// free; the loop costs register spills (hence only where it pays: the
-// widest rows, C4's shape).
+// Batches of more rows than CUs (widest rows only): every workgroup takes two
+// rows, the rows of slots w and w + G of a grid of G = ceil(n / 2) (round_row:
+// the second from the mirrored round, so that an alternating or
+// half-and-half batch of cheap and costly rows gives every workgroup one of
+// each).  MI355X's in-order dispatch of one workgroup per row left CUs idle
+// for up to 46 us between rows while another XCD had no CU free; equal pairs
+// keep the CUs of each round finishing together.  The two rows are straight
+// code, not a loop: a loop over rows spilled 232 VGPRs, the pair 103
+// (C4 176.9 -> 160.7 us).  The arguments pass through an empty asm statement
+// before each row, so that nothing derived from them is hoisted across rows
+// and held in registers.
+template <int NCH>
+__device__ __forceinline__ void one_row(FastOrGeneric &sh, const lmrs_sample_args &a0, int r) {
+  lmrs_sample_args ar = a0;
+  launder_args(ar);
+  if (!fast_row<NCH>(sh.f, ar, r)) {
+    __syncthreads();
+    generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, ar, r, 1);
+  }
+}
+
 template <int NCH>
 __global__ void __launch_bounds__(kFT) bf16_fast_rounds_kernel(lmrs_sample_args a) {
   __shared__ FastOrGeneric sh;
   const int G = (int)gridDim.x;
-  for (int slot = (int)blockIdx.x; slot < a.batch; slot += G) {
-    const int r = round_row(slot, a.batch, G);
-    // The arguments pass through an empty asm statement at every row: what
-    // the row derives from them is computed inside the loop, not hoisted out
-    // of it and held in registers across the rows (fewer spills).
-    lmrs_sample_args ar = a;
-    launder_args(ar);
-    if (!fast_row<NCH>(sh.f, ar, r)) {
-      __syncthreads();
-      generic_row<LMRS_DTYPE_BF16, kFT>(sh.g, ar, r, 1);
-    }
-    __syncthreads();  // the row's LDS views are dead
+  const int s0 = (int)blockIdx.x, s1 = s0 + G;
+  one_row<NCH>(sh, a, round_row(s0, a.batch, G));
+  if (s1 < a.batch) {
+    __syncthreads();
+    one_row<NCH>(sh, a, round_row(s1, a.batch, G));
   }
 }
 

@@ -8,7 +8,7 @@ static_assert(kFastSlotLogits == 8 * kFT && kFastVocabMax == kFastMaxVocab, "dis
 
 void launch_fast_bf16_40(const lmrs_sample_args &a, int grid, hipStream_t s) {
   if (grid < a.batch)
-    bf16_fast_rounds_kernel<40><<<dim3(grid), dim3(kFT), 0, s>>>(a);
+    launch_fast_bf16_40_pairs(a, s);  // fast_nch40_pairs.hip
   else
     bf16_fast_kernel<40><<<dim3(a.batch), dim3(kFT), 0, s>>>(a);
 }

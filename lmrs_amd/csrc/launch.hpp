@@ -15,12 +15,12 @@ constexpr int64_t kFastVocabMax = 40 * kFastSlotLogits;  // the widest instantia
 
 // bf16 rows of V <= 8 * 512 * NCH, V % 8 == 0, 16-byte aligned rows; one
 // workgroup per row, or (the widest rows, batches of more rows than `grid`,
-// the CU count) a persistent launch of `grid` workgroups taking the rows in
-// rounds
+// the CU count) two rows per workgroup
 void launch_fast_bf16_8(const lmrs_sample_args &a, int grid, hipStream_t s);
 void launch_fast_bf16_16(const lmrs_sample_args &a, int grid, hipStream_t s);
 void launch_fast_bf16_32(const lmrs_sample_args &a, int grid, hipStream_t s);
 void launch_fast_bf16_40(const lmrs_sample_args &a, int grid, hipStream_t s);
+void launch_fast_bf16_40_pairs(const lmrs_sample_args &a, hipStream_t s);  // two rows per workgroup
 // bf16 rows of any shape
 void launch_generic_bf16(const lmrs_sample_args &a, int vec, hipStream_t s);
 // f32 rows

@@ -3,7 +3,7 @@
 // Host-side argument checks, then one launch on the caller's stream (the
 // kernels live in their own translation units, behind launch.hpp): one
 // workgroup per row, or for the widest bf16 rows in batches of more rows than
-// CUs one persistent workgroup per CU.  Nothing here allocates device memory.
+// CUs two rows per workgroup.  Nothing here allocates device memory.
 #include "lmrs_sampling.h"
 #include "launch.hpp"
 
@@ -23,8 +23,8 @@ int check_args(const lmrs_sample_args *a, bool need_tokens) {
   return LMRS_OK;
 }
 
-// Workgroups of a persistent launch: one per CU of the current device
-// (queried once per device), at most one per row.
+// The CU count of the current device (queried once per device), at most the
+// number of rows: a batch of more rows than CUs pairs the widest rows.
 int fast_grid(int batch) {
   static int cus[64];
   int dev = 0;

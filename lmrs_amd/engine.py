@@ -119,19 +119,69 @@ class BatchSamplingError(S.SamplingError):
 
 
 class DecodeBatch:
-    """Samples the next token of every live sequence with one launch."""
+    """Samples the next token of every live sequence with one launch.
+
+    The live sequences' state stays on the device between steps: their
+    histories in one [live, C] uint32 buffer (row j holds sequence j's
+    generated tokens, then the padding id 0xFFFFFFFF, which is >= any vocab and
+    so ignored by the sampler as repetition.rs:93 and presence.rs:113 ignore
+    such ids), CSR offsets j * C, and the temperature / top-k / top-p arrays.
+    A step copies the uniforms in, launches, copies the four outputs back in
+    one transfer and appends the committed tokens in place; the buffers are
+    rebuilt only when the live set changes or a history reaches C (doubled
+    then)."""
+
+    _PAD = 0xFFFFFFFF
 
     def __init__(self, sequences: Seq[SequenceState]):
         self.sequences = list(sequences)
+        self._state_key = None
+        self.timings: List[float] = []  # host wall time of each step (s), launch to outputs on the host
 
     def live(self) -> List[int]:
         return [i for i, s in enumerate(self.sequences) if not s.finished]
 
+    def _device_state(self, live: List[int], dev):
+        """(hist, offsets, temperature, top_k, top_p, outputs) for the live set,
+        rebuilt when it or the capacity changed."""
+        import torch
+
+        need = max([len(self.sequences[i].generated) for i in live] + [1])
+        key = (tuple(live), dev)
+        if self._state_key == key and need < self._cap:
+            return
+        cap = 64
+        while cap <= need:
+            cap *= 2
+        n = len(live)
+        hist = torch.full((n, cap), -1, dtype=torch.int32, device=dev)  # -1 = 0xFFFFFFFF
+        for j, i in enumerate(live):
+            g = self.sequences[i].generated
+            if g:
+                hist[j, :len(g)] = torch.tensor([t if t < 2**31 else t - 2**32 for t in g], dtype=torch.int32)
+        seqs = [self.sequences[i] for i in live]
+        self._cap = cap
+        self._hist = hist
+        self._off = torch.arange(0, (n + 1) * cap, cap, dtype=torch.int64, device=dev)
+        self._temp = torch.tensor([s.params.temperature for s in seqs], dtype=torch.float64, device=dev)
+        self._topk = torch.tensor([s.params.top_k for s in seqs], dtype=torch.int32, device=dev)
+        self._topp = torch.tensor([s.params.top_p for s in seqs], dtype=torch.float64, device=dev)
+        # the four outputs as rows of one buffer: one copy back per step
+        self._outbuf = torch.empty((4, n), dtype=torch.int32, device=dev)
+        self._out = {"token_ids": self._outbuf[0], "log_probs": self._outbuf[1].view(torch.float32),
+                     "logits": self._outbuf[2].view(torch.float32), "status": self._outbuf[3]}
+        self._host = torch.empty((4, n), dtype=torch.int32, pin_memory=True)
+        self._state_key = key
+
     def step(self, logits) -> List[Optional[S.SampleOutput]]:
         """logits: [B, V] or [B, S, V] for the live sequences, in order.
         Returns one SampleOutput per sequence (None for finished ones)."""
+        import time
+
+        import numpy as np
         import torch
 
+        t0 = time.perf_counter()
         rows = last_token_logits(logits)
         live = self.live()
         if rows.shape[0] != len(live):
@@ -139,6 +189,7 @@ class DecodeBatch:
         if not live:
             return [None] * len(self.sequences)
         dev = rows.device
+        self._device_state(live, dev)
         seqs = [self.sequences[i] for i in live]
         uniforms, saved = [], []
         for s in seqs:
@@ -147,16 +198,18 @@ class DecodeBatch:
             if s.params.stochastic:
                 u, s.rng = S.next_unit(s.rng)
             uniforms.append(u)
-        off, ids = S.history_csr([s.generated for s in seqs], dev)
-        res = S.sample_batch(rows.contiguous(), hist_offsets=off, hist_ids=ids,
-                             temperature=[s.params.temperature for s in seqs],
-                             top_k=[s.params.top_k for s in seqs], top_p=[s.params.top_p for s in seqs],
-                             uniforms=uniforms)
-        torch.cuda.current_stream(dev).synchronize()
-        tok = res["token_ids"].cpu().numpy().view("uint32")
-        lp = res["log_probs"].cpu().numpy()
-        lg = res["logits"].cpu().numpy()
-        st = res["status"].cpu().numpy() & 0xFF
+        stream = torch.cuda.current_stream(dev)
+        S.sample_batch(rows.contiguous(), hist_offsets=self._off, hist_ids=self._hist,
+                       temperature=self._temp, top_k=self._topk, top_p=self._topp,
+                       uniforms=torch.tensor(uniforms, dtype=torch.float64).to(dev, non_blocking=True),
+                       out=self._out, stream=stream)
+        self._host.copy_(self._outbuf, non_blocking=True)
+        stream.synchronize()
+        h = self._host.numpy()
+        tok = h[0].view(np.uint32)
+        lp = h[1].view(np.float32)
+        lg = h[2].view(np.float32)
+        st = h[3] & 0xFF
         out: List[Optional[S.SampleOutput]] = [None] * len(self.sequences)
         # Every row's status is known before any state changes.  A failing
         # sequence keeps its generator as it was (the reference draws only
@@ -168,6 +221,7 @@ class DecodeBatch:
             if st[j] != S.ROW_OK:
                 self.sequences[i].rng = saved[j]
                 errors[i] = _ROW_MESSAGES.get(int(st[j]), f"row status {int(st[j])}")
+        app_rows, app_cols = [], []
         for j, i in enumerate(live):
             if i in errors:
                 continue
@@ -177,9 +231,19 @@ class DecodeBatch:
             if s.eos_token is not None and o.token_id == s.eos_token:
                 s.finished = True  # the EOS token is not appended (generation.rs:339-341)
             else:
+                app_rows.append(j)
+                app_cols.append(len(s.generated))
                 s.generated.append(o.token_id)
                 if len(s.generated) >= s.config.max_tokens:
                     s.finished = True
+        if app_rows:  # the committed tokens, appended on the device (where they already are)
+            jr = torch.tensor(app_rows, dtype=torch.int64).to(dev, non_blocking=True)
+            jc = torch.tensor(app_cols, dtype=torch.int64).to(dev, non_blocking=True)
+            if max(app_cols) < self._cap:
+                self._hist[jr, jc] = self._outbuf[0][jr]
+            else:
+                self._state_key = None  # a history reached the capacity: rebuilt next step
+        self.timings.append(time.perf_counter() - t0)
         if errors:
             raise BatchSamplingError(errors, out)
         return out

@@ -41,7 +41,9 @@ def asm(tmp_path_factory):
 def test_fast_kernels_have_no_load_hazards(asm):
     names = kernel_names(asm, "_ZN4lmrs16bf16_fast_kernel")
     assert len(names) == 4, names
-    for k in names:
+    pairs = kernel_names(asm, "_ZN4lmrs23bf16_fast_rounds_kernel")  # two rows per workgroup
+    assert len(pairs) == 1, pairs
+    for k in names + pairs:
         assert scan(asm, k) == [], k
 
 
