@@ -120,6 +120,18 @@ typedef struct lmrs_sample_args {
   float *log_probs;    /* ln of the chosen token's post-filter probability; 0 for greedy */
   float *logits_out;   /* processed logit of the chosen token */
   int32_t *status;     /* per-row LMRS_ROW_* code | flags */
+
+  /* Optional (NULL: not written): the post-filter distribution of each row,
+   * for tests and diagnostics (the reference exposes only the chosen token's
+   * probability, strategies/mod.rs:47-48).  kept_count[r]: the number of
+   * tokens the top-k, min-p and nucleus cuts keep (1 for Greedy, 0 for a
+   * failed row); kept_mass[r]: the sum over them of exp(f64(l - max)), l
+   * their processed logits and max the row's largest (softmax_choice's
+   * weights and sum, strategies/mod.rs:35-37).  With the processed logits
+   * (lmrs_process_logits_fwd) they give every kept token's probability:
+   * exp(f64(l - max)) / kept_mass, in the sorted order's first kept_count. */
+  int32_t *kept_count;
+  double *kept_mass;
 } lmrs_sample_args;
 
 /* Samples one token per row (the fused replacement of Sampler::sample over a

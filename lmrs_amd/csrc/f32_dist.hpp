@@ -869,7 +869,11 @@ __device__ __forceinline__ bool dist_row(GenericShared &sh, DistExtra &dx, const
         if (hi < 1.0 - 1e-15 && fabs(hi - c.u) < mg) mg = fabs(hi - c.u);
         const int32_t st = flags | (mg < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0);
         const uint32_t key = ~(uint32_t)(pk.g >> 32);
-        write_row(a, r, (uint32_t)(pk.g >> 11) & 0x3FFFFu, (float)log(pk.w / s_keep), key_value(key), st);
+        // the kept mass against the row's maximum: the weights are
+        // exp(y - R) up to f32 rounding, so divide by the maximum's (the
+        // kept count is not tracked on this path)
+        write_row(a, r, (uint32_t)(pk.g >> 11) & 0x3FFFFu, (float)log(pk.w / s_keep), key_value(key), st, -1,
+                  s_keep / (double)map.weight(M));
       }
     }
     if (generic && (threadIdx.x & 63u) == 0u) dx.generic = 1u;

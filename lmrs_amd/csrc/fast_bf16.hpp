@@ -518,7 +518,7 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
   const uint32_t lane = threadIdx.x & 63u;
   const float y = TR::value(~(uint32_t)(g >> 32));
   if (greedy) {  // Greedy: the first sorted candidate, log_prob 0, no distribution (greedy.rs:22-29)
-    if (lane == 0) write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), 0.0f, y, 0);
+    if (lane == 0) write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), 0.0f, y, 0, 1, 1.0);
     return;
   }
   const float M = TR::value(~(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(g >> 32), 0));
@@ -573,7 +573,7 @@ __device__ __forceinline__ void finish_wave(uint64_t g, const RowCfg &c, const l
     if (pick > 0u && fabs(c.u - lo) < m) m = fabs(c.u - lo);
     if (pick + 1u < keep && fabs(hi - c.u) < m) m = fabs(hi - c.u);
     write_row(a, r, (uint32_t)(g & 0xFFFFFFFFu), (float)log(w * rkeep), y,
-              flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+              flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0), (int32_t)keep, sum_keep);
   }
 }
 
@@ -1127,7 +1127,11 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   int last_e = hg - 1, last_h = nb;
   uint32_t last_keep = 0u;
   double cand_mass = total;
+  // the kept count (every element when no cut applies; -1 where a cut falls
+  // among the negligible elements, whose keys the window does not count)
+  int64_t kept_n = a.vocab;
   if (k_on) {
+    kept_n = c.top_k;  // top-k keeps k tokens (k < V)
     int f = 0x7FFFFFFF;
     if (tid < hg && cincl[tid] >= (uint32_t)c.top_k) f = tid;
     f = block_min<kFW>(f, sh.iscr);
@@ -1165,8 +1169,11 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
         last_h = group_head(last_e);
         last_keep = cnt_excl(last_e) + cnt_of(last_e) - cnt_excl(last_h);
         cand_mass = mincl[last_e];
+        kept_n = cincl[last_e];
       } else if (!tail_negligible) {
         return false;
+      } else {
+        kept_n = -1;
       }
     }
     if (minp_near(key16_value(ymp), M, thr) || (ymp > kNegInfKey16 && minp_near(key16_value(ymp - 1u), M, thr)))
@@ -1189,6 +1196,7 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
     if (jj > (double)gmax) jj = (double)gmax;
     const uint32_t jp = (uint32_t)jj;
     kept_mass = mx2 + (double)jp * wg;
+    kept_n = (int64_t)cnt_excl(h) + jp;
     const double acc = kept_mass / cand_mass, prev = (kept_mass - wg) / cand_mass;
     double m = c.top_p - prev;
     if (acc - c.top_p < m) m = acc - c.top_p;
@@ -1221,7 +1229,8 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
     double m = 1.0;
     if (!first_tok && fabs(c.u - lo_c) < m) m = fabs(c.u - lo_c);
     if (!last_tok && fabs(hi_c - c.u) < m) m = fabs(hi_c - c.u);
-    write_row(a, r, token, (float)log(wg / kept_mass), yv, flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+    write_row(a, r, token, (float)log(wg / kept_mass), yv, flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0),
+              (int32_t)kept_n, kept_mass);
   }
   return true;
 }
@@ -1344,10 +1353,12 @@ __device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_
   const float M = key16_value(ymax);
   if (c.greedy) {  // Greedy (greedy.rs:22-29): the lowest index at the maximum, log_prob 0
     const uint32_t tok = uniform(binmin[bmax]);
-    if (lane == 0u) write_row(a, r, tok, 0.0f, M, LMRS_ROW_OK);
+    if (lane == 0u) write_row(a, r, tok, 0.0f, M, LMRS_ROW_OK, 1, 1.0);
     return true;
   }
   const double w = in ? ((const double *)sh.u32(kLOffWbin))[gb] : 0.0;  // exp(y - y0) per token
+  const bool dist = a.kept_count || a.kept_mass;  // the post-filter distribution is asked for
+  const uint32_t cnt_incl = dist ? wave_inclusive<OpSum>(in ? gcnt : 0u, 0u) : 0u;  // tokens of groups 0 .. lane
   const double rw = in ? 1.0 / w : 0.0;
   const double incm = wave_inclusive<OpSum>(w * (double)gcnt, 0.0);
   const double excl = incm - w * (double)gcnt;
@@ -1417,6 +1428,11 @@ __device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_
   const uint32_t jt = (uint32_t)jj;
   const uint32_t gbf = (uint32_t)__builtin_amdgcn_readlane((int)gb, (int)f), ykf = y0 + gbf;
   const uint32_t tok = jt == 1u ? uniform(binmin[gbf]) : stream_nth_index(sh, ykf, jt);
+  // the kept set: groups before `last` whole, then last_keep tokens (the
+  // prefix sum runs with every lane active, outside the branch below); its
+  // mass against the row's maximum, group 0's weight exp(M - y0)
+  const uint32_t before = dist && last > 0u ? (uint32_t)__builtin_amdgcn_readlane((int)cnt_incl, (int)(last - 1u)) : 0u;
+  const double w0 = dist ? at(w, 0u) : 1.0;
   if (lane == 0u) {
     // ln(w / kept) = (y - y0) - ln(kept), the difference exact in f32; ln(kept)
     // from log2 of its mantissa in [0.5, 1) (within 1e-7) and its exponent
@@ -1431,7 +1447,7 @@ __device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_
     if (!(f == last && jt == gmax) && fabs(hi_c - c.u) < m) m = fabs(hi_c - c.u);
     if (!hit) m = 0.0;
     write_row(a, r, tok, (float)((double)(yv - key16_value(y0)) - lnk), yv,
-              flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+              flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0), (int32_t)(before + last_keep), kept / w0);
   }
   return true;
 }
@@ -2244,6 +2260,7 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
   const uint32_t zhi = uniform(ent[h] >> 16), zlo = uniform(ent[tl] >> 16);
   const float yv = key16_value(ykey_of(h));
   const bool first_tok = (h == 0 && jt == 1u), last_tok = (h == last_h && jt == gmax);
+  const uint32_t kept_n = uniform(cnt_excl(last_h) + last_keep);  // every key is counted here
   __syncthreads();  // entries and prefixes are dead
   if (nmem) {
     uint32_t *wi = sh.m_idx(), *wk = sh.m_key();
@@ -2264,7 +2281,8 @@ __device__ __forceinline__ bool fast_row(FastShared &sh, const lmrs_sample_args 
     if (!first_tok && fabs(c.u - lo_c) < m) m = fabs(c.u - lo_c);
     if (!last_tok && fabs(hi_c - c.u) < m) m = fabs(hi_c - c.u);
     if (ovf) m = 0.0;
-    write_row(a, r, token, (float)log(wg / kept_mass), yv, flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0));
+    write_row(a, r, token, (float)log(wg / kept_mass), yv, flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0),
+              (int32_t)kept_n, kept_mass);
   }
   return true;
 }

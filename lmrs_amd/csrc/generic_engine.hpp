@@ -310,12 +310,20 @@ __device__ __forceinline__ WeightSel select_by_weight(SelState &ss, const Row &r
 }
 
 // Writes one row's outputs (thread 0 only).
+// One row's outputs.  kept / mass: the post-filter distribution's size and
+// sum of exp(l - max) (lmrs_sample_args::kept_count, kept_mass); a failed row
+// writes 0 and 0; a sampled row whose path does not pass them writes -1
+// ("not reported", which the tests count).
 __device__ __forceinline__ void write_row(const lmrs_sample_args &a, int r, uint32_t token,
-                                          float log_prob, float logit, int32_t status) {
+                                          float log_prob, float logit, int32_t status,
+                                          int32_t kept = -1, double mass = 0.0) {
   a.token_ids[r] = token;
   if (a.log_probs) a.log_probs[r] = log_prob;
   if (a.logits_out) a.logits_out[r] = logit;
   if (a.status) a.status[r] = status;
+  const bool failed = (status & 0xFF) != LMRS_ROW_OK;
+  if (a.kept_count) a.kept_count[r] = failed ? 0 : kept;
+  if (a.kept_mass) a.kept_mass[r] = failed ? 0.0 : mass;
 }
 
 // Sorts ss.gather[0..n) ascending (bitonic; n <= kGatherCap).  Barriers inside.
@@ -356,7 +364,7 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
   constexpr int P = kGatherCap / NT, NW = NT / 64;
   const float M = TR::value(~uniform((uint32_t)(ss.gather[0] >> 32)));
   if (c.greedy) {  // Greedy (greedy.rs:22-29): the first sorted candidate, no distribution
-    if (threadIdx.x == 0) write_row(a, r, (uint32_t)(ss.gather[0] & 0xFFFFFFFFu), 0.0f, M, LMRS_ROW_OK);
+    if (threadIdx.x == 0) write_row(a, r, (uint32_t)(ss.gather[0] & 0xFFFFFFFFu), 0.0f, M, LMRS_ROW_OK, 1, 1.0);
     return;
   }
   int32_t flags = 0;
@@ -456,7 +464,7 @@ __device__ __forceinline__ void finish_sorted(SelState &ss, const RowCfg &c, con
       if (i > 0 && fabs(c.u - lo) < m) m = fabs(c.u - lo);
       if (i + 1u < keep && fabs(hi - c.u) < m) m = fabs(hi - c.u);
       const int32_t st = flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0);
-      write_row(a, r, token, (float)log(wv[q] / sum_keep), y, st);
+      write_row(a, r, token, (float)log(wv[q] / sum_keep), y, st, (int32_t)keep, sum_keep);
     }
   }
 }
@@ -488,7 +496,7 @@ __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const R
   using TR = typename Row::TR;
   const float M = TR::value(kmax);
   if (c.greedy) {  // Greedy (greedy.rs:22-29): sorted[0], log_prob 0
-    if (threadIdx.x == 0) write_row(a, r, imax, 0.0f, M, LMRS_ROW_OK);
+    if (threadIdx.x == 0) write_row(a, r, imax, 0.0f, M, LMRS_ROW_OK, 1, 1.0);
     return;
   }
   const bool k_on = c.top_k > 0 && c.top_k < V;
@@ -584,7 +592,8 @@ __device__ __forceinline__ void select_row(SelState &ss, const Row &row, const R
     if (hi < 1.0 - 1e-15 && fabs(hi - c.u) < m) m = fabs(hi - c.u);
     if (d.overflow) m = 0.0;
     const int32_t st = flags | (m < 1e-6 ? LMRS_ROW_NEAR_BOUNDARY : 0);
-    write_row(a, r, token, (float)log(w_exact / d.total), y, st);
+    // (the kept count is not tracked on this path: its cuts are key thresholds)
+    write_row(a, r, token, (float)log(w_exact / d.total), y, st, -1, d.total);
   }
 }
 

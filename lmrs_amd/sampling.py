@@ -54,6 +54,8 @@ class SampleArgs(ctypes.Structure):
         ("log_probs", ctypes.c_void_p),
         ("logits_out", ctypes.c_void_p),
         ("status", ctypes.c_void_p),
+        ("kept_count", ctypes.c_void_p),
+        ("kept_mass", ctypes.c_void_p),
     ]
 
 
@@ -159,10 +161,11 @@ class PreparedBatch:
 
 def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
                   presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
-                  top_p=None, uniforms=None, min_p=None, out=None) -> PreparedBatch:
+                  top_p=None, uniforms=None, min_p=None, out=None, dist: bool = False) -> PreparedBatch:
     """Validates the host-side shapes and builds the argument block of
     ``lmrs_sample_fwd`` (per-row parameters as tensors or sequences of length
-    B, None = neutral)."""
+    B, None = neutral).  dist: also return each row's post-filter
+    distribution size and mass (``kept_count``, ``kept_mass``)."""
     torch = _torch()
     if logits.dim() != 2:
         raise ValueError("logits must be [batch, vocab]")
@@ -188,19 +191,23 @@ def prepare_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalt
             "logits": torch.empty(B, dtype=torch.float32, device=dev),
             "status": torch.empty(B, dtype=torch.int32, device=dev),
         }
+    if dist and "kept_count" not in out:
+        out["kept_count"] = torch.empty(B, dtype=torch.int32, device=dev)
+        out["kept_mass"] = torch.empty(B, dtype=torch.float64, device=dev)
     args = SampleArgs(
         logits=_ptr(logits), dtype=dt, batch=B, vocab=V, row_stride=logits.stride(0) if B > 0 else V,
         hist_offsets=_ptr(hist_offsets), hist_ids=_ptr(hist_ids), repetition_penalty=_ptr(rp),
         presence_penalty=_ptr(pp), frequency_penalty=_ptr(fp), temperature=_ptr(tt), top_k=_ptr(tk),
         top_p=_ptr(tp), uniforms=_ptr(uu), min_p=_ptr(mp), token_ids=_ptr(out["token_ids"]),
         log_probs=_ptr(out["log_probs"]), logits_out=_ptr(out["logits"]), status=_ptr(out["status"]),
+        kept_count=_ptr(out.get("kept_count")), kept_mass=_ptr(out.get("kept_mass")),
     )
     return PreparedBatch(args, out, (logits, rp, pp, fp, tt, tk, tp, uu, mp, hist_offsets, hist_ids))
 
 
 def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty=None,
                  presence_penalty=None, frequency_penalty=None, temperature=None, top_k=None,
-                 top_p=None, uniforms=None, min_p=None, stream=None, out=None):
+                 top_p=None, uniforms=None, min_p=None, stream=None, out=None, dist: bool = False):
     """Samples one token per row of a [B, V] bf16/f32 CUDA tensor.
 
     Per-row parameters are tensors or sequences of length B (None = neutral;
@@ -212,7 +219,7 @@ def sample_batch(logits, *, hist_offsets=None, hist_ids=None, repetition_penalty
     pb = prepare_batch(logits, hist_offsets=hist_offsets, hist_ids=hist_ids,
                        repetition_penalty=repetition_penalty, presence_penalty=presence_penalty,
                        frequency_penalty=frequency_penalty, temperature=temperature, top_k=top_k,
-                       top_p=top_p, uniforms=uniforms, min_p=min_p, out=out)
+                       top_p=top_p, uniforms=uniforms, min_p=min_p, out=out, dist=dist)
     s = stream if stream is not None else torch.cuda.current_stream(logits.device)
     _on_stream(s, list(pb._keep) + [v for k, v in pb.out.items() if k != "_keep"])
     pb.launch(s)

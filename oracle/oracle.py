@@ -253,5 +253,6 @@ def sample_batch(logits: np.ndarray, hist_offsets, hist_ids, params_list, unifor
         "min_p_margin": np.array([d.min_p_margin for d in diags]),
         "n_candidates": np.array([d.n_candidates for d in diags]),
         "n_kept": np.array([d.n_kept for d in diags]),
+        "sum_kept": np.array([d.sum_kept for d in diags]),
         "prob": np.array([d.weight / d.sum_kept if d.sum_kept > 0 else np.nan for d in diags]),
     }

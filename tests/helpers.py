@@ -35,13 +35,15 @@ def run_gpu(w, logits=None, off=None, ids=None):
     res = S.sample_batch(logits, hist_offsets=off, hist_ids=ids, repetition_penalty=w.repetition_penalty,
                          presence_penalty=w.presence_penalty, frequency_penalty=w.frequency_penalty,
                          temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, uniforms=w.uniforms,
-                         min_p=w.min_p)
+                         min_p=w.min_p, dist=True)
     torch.cuda.synchronize()
     return {
         "token_id": res["token_ids"].cpu().numpy().view(np.uint32),
         "log_prob": res["log_probs"].cpu().numpy(),
         "logit": res["logits"].cpu().numpy(),
         "status": res["status"].cpu().numpy(),
+        "kept_count": res["kept_count"].cpu().numpy(),
+        "kept_mass": res["kept_mass"].cpu().numpy(),
     }
 
 
@@ -84,7 +86,20 @@ def compare(gpu, ref):
     mg = np.minimum(ref["cdf_margin"], ref["top_p_margin"])
     must = ok & ((mg < 0.5 * BOUNDARY) | (ref["min_p_margin"] < 0.5 * MINP_BOUNDARY))
     must_not = ok & (mg > 2 * BOUNDARY) & np.isinf(ref["min_p_margin"])
+    # the post-filter distribution (kept count and mass, when the GPU reports
+    # them): every kept token's probability is exp(l - max) / mass over the
+    # first `count` of the sorted order, so these two pin all of them
+    dist = {}
+    if "kept_count" in gpu:
+        clean = ok & ~boundary
+        kc, km = gpu["kept_count"], gpu["kept_mass"]
+        counted = clean & (kc >= 0)
+        mrel = np.abs(km - ref["sum_kept"]) / np.maximum(np.abs(ref["sum_kept"]), 1e-300)
+        dist = {"kept_count_mismatch": int(np.sum(counted & (kc != ref["n_kept"]))),
+                "kept_count_unreported": int(np.sum(clean & (kc < 0))),
+                "kept_mass_max_rel_err": float(np.max(np.where(clean, mrel, 0.0))) if len(ok) else 0.0}
     return {
+        **dist,
         "rows": int(len(ok)),
         "status_mismatch": status_mismatch,
         "token_mismatch": int(np.sum(mism)),
@@ -105,3 +120,6 @@ def assert_parity(rep, name=""):
     assert rep["logit_mismatch"] == 0, (name, rep)
     assert rep["max_prob_rel_err"] < PROB_RTOL, (name, rep)
     assert rep["flag_missing"] == 0 and rep["flag_extra"] == 0, (name, rep)
+    if "kept_count_mismatch" in rep:
+        assert rep["kept_count_mismatch"] == 0, (name, rep)
+        assert rep["kept_mass_max_rel_err"] < PROB_RTOL, (name, rep)
