@@ -958,10 +958,11 @@ constexpr int kOffWinHist = 4096;              // views inside the SelState regi
 constexpr int kOffWinKey = kOffWinHist + kWin * 4;
 constexpr int kOffWinCnt = kOffWinKey + kWin * 4;
 constexpr int kOffWinMass = kOffWinCnt + kWin * 4;
+constexpr int kOffWinBinMin = kOffWinMass + kWin * 8;  // per bin, its lowest index (compacted rows)
 constexpr int kOffWinList = 16 * 1024;          // the listed chunks' keys, then their indices
 constexpr int kWinListCap = 2048;
 constexpr int kOffWinListCh = kOffWinList + kWinListCap * 16;
-static_assert(kOffTcnt + kFT * 4 <= kOffWinHist && kOffWinMass + kWin * 8 <= kOffWinList &&
+static_assert(kOffTcnt + kFT * 4 <= kOffWinHist && kOffWinBinMin + kWin * 4 <= kOffWinList &&
               kOffWinListCh + kWinListCap * 4 <= kOffWhist, "window views");
 
 // Returns false (uniformly, with the registers and the member list intact)
@@ -971,7 +972,7 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
                                             const uint32_t (&k)[NCH][4], int nchunks, uint32_t nmem, bool hist,
                                             uint32_t mx, uint32_t zmem, uint32_t zlow_max, bool k_on) {
   const int tid = threadIdx.x;
-  const uint32_t *mkey = sh.m_key();
+  const uint32_t *mkey = sh.m_key(), *midx = sh.m_idx();
   // no element's z key exceeds this: the raw chunk maxima (members' raw keys
   // included) and the members' z keys
   const uint32_t zhb = block_max<kFW>(max(mx, zmem), sh.uscr);
@@ -1005,8 +1006,10 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   const bool tail_negligible = zlo == zskip;
   // weight exp(y - Mb) as exp2(y log2(e) - Mb log2(e)), one multiply-add
   const float l2e = 1.4426950408889634f, mb2 = Mb * l2e;
-  uint32_t *wh = sh.u32(kOffWinHist);
+  uint32_t *wh = sh.u32(kOffWinHist), *wmin = sh.u32(kOffWinBinMin);
   wh[tid] = 0u;
+  wmin[tid] = 0xFFFFFFFFu;
+  bool track_min = false;  // (uniform) the bins' lowest indices are kept: the compacted pass
   // One chunk's window counts (by LDS atomics) and the weight sum of its
   // elements below the window.
   auto window_chunk = [&](const uint4 &w, uint32_t ch) {
@@ -1017,7 +1020,10 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
     for (int e = 0; e < 8; ++e) {
       const uint32_t key = (x[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
       const bool mem = (m8 >> e) & 1u;
-      if (!mem && key >= zlo) atomicAdd(&wh[zhb - key], 1u);
+      if (!mem && key >= zlo) {
+        atomicAdd(&wh[zhb - key], 1u);
+        if (track_min) atomicMin(&wmin[zhb - key], ch * 8u + (uint32_t)e);
+      }
       const float wt = __builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(key, c)), l2e, -mb2));
       acc += (mem || key >= zlo || key < zskip) ? 0.0f : wt;
     }
@@ -1041,6 +1047,7 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
     __syncthreads();
   double below = 0.0;
   if (nlive <= (uint32_t)kWinListCap) {
+    track_min = true;
     uint4 *lk = (uint4 *)sh.u32(kOffWinList);
     uint32_t *lc = sh.u32(kOffWinListCh), p = lpos;
     static_for<0, NCH>([&](auto S) {
@@ -1062,9 +1069,10 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   }
   for (uint32_t m = tid; m < nmem; m += kFT) {
     const uint32_t zk = mkey[m] >> 16;
-    if (zk >= zlo)
+    if (zk >= zlo) {
       atomicAdd(&wh[zhb - zk], 1u);
-    else if (zk >= zskip)
+      if (track_min) atomicMin(&wmin[zhb - zk], midx[m]);
+    } else if (zk >= zskip)
       below += (double)__builtin_amdgcn_exp2f(__builtin_fmaf(key16_value(temp_key16(zk, c)), l2e, -mb2));
   }
   below = block_sum<kFW>(below, sh.dscr);  // (its barriers order the histogram too)
@@ -1220,9 +1228,16 @@ __device__ __forceinline__ bool full_window(FastShared &sh, const lmrs_sample_ar
   const uint32_t gtot = uniform(cincl[tl] - cnt_excl(h));  // the group's elements
   const float yv = key16_value(ykey_of(h));
   const bool first_tok = (h == 0 && jt == 1u), last_tok = (h == last_h && jt == gmax);
+  // the first token of its tie group: the lowest index over the group's bins
+  uint32_t token = ~0u;
+  if (track_min && jt == 1u) {
+    for (int e = h; e <= tl; ++e) token = min(token, wmin[zhb - ekey[e]]);
+    token = uniform(token);
+  }
   if (tid == 0) sh.counters()[kCtrList] = 0u;
   __syncthreads();  // the window views are dead
-  uint32_t token = gtot <= (uint32_t)kListCap ? find_jth_list<NCH>(sh, k, nmem, hist, zlo2, zhi, jt) : ~0u;
+  if (token == ~0u)
+    token = gtot <= (uint32_t)kListCap ? find_jth_list<NCH>(sh, k, nmem, hist, zlo2, zhi, jt) : ~0u;
   if (token == ~0u) token = find_jth_regs<NCH>(sh, k, nchunks, nmem, zlo2, zhi, jt);
   if (tid == 0) {
     const double lo_c = (mx2 + (double)(jt - 1u) * wg) / kept_mass, hi_c = lo_c + wg / kept_mass;
