@@ -279,7 +279,7 @@ constexpr int kOffMatch = kOffGroups + 64 * 8;
 constexpr int kCtrLeanBad = 6;           // counters() words of the lean pass: a reason to decline,
 constexpr int kCtrLeanYmax = 7;          // and the largest listed y key
 constexpr int kLOffWbin = 64 * 1024;     // lean pass: exp(y - y0) of each candidate bin (f64)
-constexpr int kFinishBins = 256;         // the bins stream_finish scans below the largest key
+constexpr int kFinishBins = kCandBins;   // the bins stream_finish scans below the largest key (all)
 static_assert(kLOffHash + kLHashSlots * 4 <= kLOffRecRaw && kLOffBinMin + kCandBins * 4 <= kOffCand, "lean views");
 static_assert(kOffMatch + kFW * kCandSeg * 4 <= kOffWhist, "candidate views");
 static_assert(kFastHistory * 2 <= kLHashSlots && kFastMaxVocab < (1 << 18) && kFastHistory < (1 << 14),
@@ -1332,8 +1332,10 @@ __device__ __forceinline__ bool stream_finish(FastShared &sh, const lmrs_sample_
   const uint32_t *hb = sh.u32(kOffCandHist);
   uint32_t base = 0u, G = 0u, keep_k = 0u, packed = 0u;
   bool found = false;
-  static_assert(kFinishBins == 4 * 64, "four rounds of 64 bins");
-  for (int e = 0; e < 4 && !found; ++e) {
+  // (all the candidate bins: with 256, heavy-tailed rows whose K-th token lay
+  // further below the maximum declined and were read again)
+  static_assert(kFinishBins == 8 * 64, "eight rounds of 64 bins");
+  for (int e = 0; e < kFinishBins / 64 && !found; ++e) {
     const int bl = (int)bmax - (int)lane - 64 * e;
     const uint32_t cnt = bl >= 0 ? hb[bl] : 0u;
     const uint32_t incl = wave_inclusive<OpSum>(cnt, 0u) + base;
