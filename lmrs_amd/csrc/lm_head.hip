@@ -13,22 +13,32 @@
 //
 // Layout: a workgroup of four waves owns 128 vocabulary columns and up to 256
 // rows (wave w: rows 64 w .. 64 w + 63, in four 16-row blocks; eight 16-column
-// blocks: 32 MFMA accumulators of four floats per lane).  Each lane reads its
-// operands straight from HBM/L2 as 16-byte loads (eight bf16 along k): lane l
-// of a block holds row (or column) l % 16 and k = 8 (l / 16) .. + 7, the
-// operand layout of the 16x16x32 bf16 MFMA, whose result gives lane l the
-// column l % 16 and rows 4 (l / 16) .. + 3.  The weight matrix (the bytes
-// that bound the projection) is read once per launch; the four waves of a
-// workgroup read the same weight fragments, served by the CU's L1 after the
-// first.  The k loop keeps the next kLhDepth steps' fragments in flight while
-// a step's 32 MFMAs run (with one step in flight the projection was bound by
-// the loads' latency: 807 us at 256 x 4096 x 128256).
+// blocks: 32 MFMA accumulators of four floats per lane).  The operand layout
+// of the 16x16x32 bf16 MFMA: lane l of a block holds row (or column) l % 16
+// and k = 8 (l / 16) .. + 7; the result gives lane l the column l % 16 and
+// rows 4 (l / 16) .. + 3.
+//
+// The k loop runs over tiles of 64 k.  The weight tile (128 columns x 64 k,
+// 16 KiB: the bytes that bound the projection, read from HBM once per
+// launch) is loaded once per workgroup, each thread fetching four 16-byte
+// chunks, and stored to LDS, where the four waves read their B fragments;
+// columns are padded to 144 bytes so the 16 lanes reading one k chunk of
+// 16 consecutive columns spread over the banks.  Two LDS buffers alternate
+// (one read by the MFMAs while the next tile is stored to the other, one
+// barrier per tile), and the weight loads run two tiles ahead of the MFMAs
+// in two register sets.  Each wave's x fragments (its own rows, from L2)
+// are loaded one tile ahead.  Measured at 256 x 4096 x 128256: 799 us with
+// each wave loading its own weight fragments, 567 us with the LDS tile, 527
+// us with the reduction below on DPP and the loads two tiles ahead (a
+// plain hipBLASLt GEMM of the same shape, without the epilogue: 336 us).
 //
 // Epilogue: the logits are rounded to bf16 (round to nearest even) and
 // stored, and for every row the largest logit of each 64-column tile is
 // reduced across the lanes that hold it, in the sampler's total order
 // (the key of crates/sampling/src/strategies/mod.rs:21-25's total_cmp, ties
-// to the lower column): tile_max[r, t] = key << 32 | ~column.  The row
+// to the lower column): tile_max[r, t] = key << 32 | ~column.  The
+// reduction runs on 32-bit entries key << 16 | (0xFFFF - column % 64), which
+// order as the stored form does, over the 16 lanes of a DPP row.  The row
 // maximum and greedy's token are the maximum of a row's tile entries; the
 // tile maxima also bound a top-k cut from below, without a read of the logits.
 #include <hip/hip_runtime.h>
@@ -50,7 +60,6 @@ constexpr int kLhRows = kLhRowsPerWave * kLhWaves;    // rows of one workgroup (
 constexpr int kLhCols = 128;                          // eight 16-column blocks
 constexpr int kLhRB = kLhRowsPerWave / 16, kLhCB = kLhCols / 16;
 constexpr int kLhStep = 32;                           // k per MFMA
-constexpr int kLhDepth = 4;                           // k steps of fragments in flight
 constexpr int kTileCols = 64;                         // columns per tile_max entry
 
 // Total-order key of a bf16 pattern (larger key = later in the reference's
@@ -58,6 +67,8 @@ constexpr int kTileCols = 64;                         // columns per tile_max en
 __device__ __forceinline__ uint32_t bf16_key(uint32_t b) {
   return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
 }
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
 // Eight bf16 of row `p` from k (zeros where the row or k is out of range).
 __device__ __forceinline__ bf16x8 load8(const uint16_t *base, int64_t ld, int row, int nrows, int k, int K) {
@@ -68,10 +79,24 @@ __device__ __forceinline__ bf16x8 load8(const uint16_t *base, int64_t ld, int ro
   return __builtin_bit_cast(bf16x8, u32x4v{0u, 0u, 0u, 0u});
 }
 
+// The weight tile of kLhTileK k (kLhCols columns, bf16) in LDS, one
+// 128-byte column every kLhColStride bytes (padded against bank conflicts);
+// two buffers, one filled while the other is read.  A tile holds two MFMA
+// k steps.
+constexpr int kLhTileK = 2 * kLhStep;
+constexpr int kLhColStride = kLhTileK * 2 + 16;
+constexpr int kLhTileBytes = kLhCols * kLhColStride;
+constexpr int kLhColChunks = kLhTileK / 8;                  // 16-byte chunks of a column
+constexpr int kLhChunks = kLhCols * kLhColChunks;            // 16-byte chunks of a tile
+constexpr int kLhChunksPer = kLhChunks / kLhThreads;        // per thread
+static_assert(kLhChunks % kLhThreads == 0, "tile chunks per thread");
+
 __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ x,
                                                            const uint16_t *__restrict__ w, int rows, int K, int V,
                                                            uint64_t *__restrict__ tile_max) {
-  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) unsigned char wt[2][kLhTileBytes];
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int col0 = (int)blockIdx.x * kLhCols;
   const int row0 = (int)blockIdx.y * kLhRows + wave * kLhRowsPerWave;
   const int li = lane & 15, lk = (lane >> 4) * 8;  // operand row/column in a block, k offset
@@ -82,28 +107,71 @@ __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restric
 #pragma unroll
     for (int j = 0; j < kLhCB; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // kLhDepth k steps of fragments in flight: step d of each group of
-  // kLhDepth steps uses register set d, which is refilled with the step
-  // kLhDepth ahead right after its MFMAs (the compiler waits for each set's
-  // own loads only).  Steps past K load zeros.
-  bf16x8 a[kLhDepth][kLhRB], b[kLhDepth][kLhCB];
-  auto fetch = [&](int k0, bf16x8 (&fa)[kLhRB], bf16x8 (&fb)[kLhCB]) {
+  // this thread's chunks of the weight tile: column c / kLhColChunks, k chunk
+  // c % kLhColChunks.  Two register sets: the tile two ahead is in flight in
+  // one while the other (the next tile, issued an iteration earlier) lands
+  // and is stored to LDS.  Chunks past K load a clamped address (in bounds:
+  // K > 0 is a multiple of 8) and store zeros; a per-lane guard on the loads
+  // instead cost 75 us at 256 x 4096 x 128256.
+  u32x4v w0[kLhChunksPer], w1[kLhChunksPer];
+  auto fetch_w = [&](int k0, u32x4v (&wr)[kLhChunksPer]) {
 #pragma unroll
-    for (int i = 0; i < kLhRB; ++i) fa[i] = load8(x, K, row0 + 16 * i + li, rows, k0 + lk, K);
-#pragma unroll
-    for (int j = 0; j < kLhCB; ++j) fb[j] = load8(w, K, col0 + 16 * j + li, V, k0 + lk, K);
+    for (int q = 0; q < kLhChunksPer; ++q) {
+      const int c = tid + q * kLhThreads, col = col0 + c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
+      const int cc = col < V ? col : V - 1, kc = k < K ? k : 0;
+      wr[q] = *(const u32x4v *)(w + (int64_t)cc * K + kc);
+    }
   };
+  auto store_w = [&](int k0, const u32x4v (&wr)[kLhChunksPer], int buf) {
 #pragma unroll
-  for (int d = 0; d < kLhDepth; ++d) fetch(d * kLhStep, a[d], b[d]);
-  for (int k0 = 0; k0 < K; k0 += kLhDepth * kLhStep) {
+    for (int q = 0; q < kLhChunksPer; ++q) {
+      const int c = tid + q * kLhThreads, col = col0 + c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
+      const u32x4v z = {0u, 0u, 0u, 0u};
+      *(u32x4v *)&wt[buf][(c / kLhColChunks) * kLhColStride + (c % kLhColChunks) * 16] = (col < V && k < K) ? wr[q] : z;
+    }
+  };
+  bf16x8 a[2][kLhRB], an[2][kLhRB];
+  auto fetch_x = [&](int k0, bf16x8 (&fa)[2][kLhRB]) {
 #pragma unroll
-    for (int d = 0; d < kLhDepth; ++d) {
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kLhRB; ++i) fa[h][i] = load8(x, K, row0 + 16 * i + li, rows, k0 + h * kLhStep + lk, K);
+  };
+  // one tile: issue tile t + 2's weights into `wfill` and tile t + 1's x,
+  // run tile t's MFMAs from LDS buffer `buf`, store tile t + 1 (in `wland`)
+  // to the other buffer
+  auto tile = [&](int k0, u32x4v (&wfill)[kLhChunksPer], const u32x4v (&wland)[kLhChunksPer], int buf) {
+    fetch_w(k0 + 2 * kLhTileK, wfill);
+    fetch_x(k0 + kLhTileK, an);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 b[kLhCB];
+#pragma unroll
+      for (int j = 0; j < kLhCB; ++j)
+        b[j] = __builtin_bit_cast(
+            bf16x8, *(const u32x4v *)&wt[buf][(16 * j + li) * kLhColStride + h * 64 + (lane >> 4) * 16]);
 #pragma unroll
       for (int i = 0; i < kLhRB; ++i)
 #pragma unroll
         for (int j = 0; j < kLhCB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d][i], b[d][j], acc[i][j], 0, 0, 0);
-      fetch(k0 + (d + kLhDepth) * kLhStep, a[d], b[d]);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h][i], b[j], acc[i][j], 0, 0, 0);
+    }
+    store_w(k0 + kLhTileK, wland, buf ^ 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < kLhRB; ++i) a[h][i] = an[h][i];
+    __syncthreads();  // the other buffer is written; this one's reads are done
+  };
+  if (K > 0) {  // (K = 0: no weight row to clamp to; the logits are zeros)
+    fetch_w(0, w0);
+    fetch_x(0, a);
+    fetch_w(kLhTileK, w1);
+    store_w(0, w0, 0);
+    __syncthreads();
+    for (int k0 = 0; k0 < K; k0 += 2 * kLhTileK) {
+      tile(k0, w0, w1, 0);
+      if (k0 + kLhTileK < K) tile(k0 + kLhTileK, w1, w0, 1);
     }
   }
 
@@ -115,29 +183,34 @@ __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restric
     for (int q = 0; q < 4; ++q) {
       const int row = row0 + 16 * i + 4 * (lane >> 4) + q;
       // per 64-column tile (blocks 0-3 and 4-7): this lane's best of its four columns
-      uint64_t best[2] = {0u, 0u};
+      uint32_t best[2] = {0u, 0u};
 #pragma unroll
       for (int j = 0; j < kLhCB; ++j) {
         const int col = col0 + 16 * j + li;
         const uint32_t bits = f32_to_bf16_dev(acc[i][j][q]);
         if (row < rows && col < V) {
           out[(int64_t)row * V + col] = (uint16_t)bits;
-          const uint64_t e = ((uint64_t)bf16_key(bits) << 32) | (uint32_t)~(uint32_t)col;
+          const uint32_t e = (bf16_key(bits) << 16) | (0xFFFFu - (uint32_t)(col % kTileCols));
           best[j / 4] = e > best[j / 4] ? e : best[j / 4];
         }
       }
       if (tile_max) {
-        // across the 16 lanes of this row (lanes 16 g .. 16 g + 15)
+        // across the 16 lanes of this row (lanes 16 g .. 16 g + 15, one DPP
+        // row): 32-bit entries key << 16 | (0xFFFF - column % 64), the same
+        // order as the stored form; quad swaps, then the half-row and row
+        // mirrors reach all 16 lanes.  Out-of-range lanes hold 0.
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          uint64_t v = best[t];
-#pragma unroll
-          for (int off = 8; off >= 1; off >>= 1) {
-            const uint64_t o = (uint64_t)__shfl_xor((unsigned long long)v, off, 16);
-            v = o > v ? o : v;
-          }
+          uint32_t v = best[t];
+          v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+          v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+          v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+          v = umax32(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
           const int tile = (col0 / kTileCols) + t;
-          if (li == 0 && row < rows && tile < ntiles && v != 0u) tile_max[(int64_t)row * ntiles + tile] = v;
+          if (li == 0 && row < rows && tile < ntiles && v != 0u) {
+            const uint32_t col = (uint32_t)(tile * kTileCols) + (0xFFFFu - (v & 0xFFFFu));
+            tile_max[(int64_t)row * ntiles + tile] = ((uint64_t)(v >> 16) << 32) | (uint32_t)~col;
+          }
         }
       }
     }
