@@ -233,9 +233,11 @@ __device__ __forceinline__ uint32_t penalise_member(uint32_t raw, uint32_t count
 // greedy and small-k rows (lean_row):
 //   [0, 32K)      history hash: token + 1 | multiplicity << 18
 //   [32K, 42K)    per wave, the chunks it recorded: raw words, chunk index
+//   [42K, 44K)    per candidate bin, its lowest index
 //   [44K, 59K)    per wave, its candidates (y key << 32 | index); the count
 //                 histogram over y keys from the bound; the finishing wave's
 //                 group table and index scratch
+//   [64K, 68K)    per candidate bin, exp(y - y0) (f64)
 // The general pass of every other row (and of a lean row that declines):
 //   [0, 10K)      per bitmap word, the number of members before it (history
 //                 build); then [0, 57K) SelState: candidate list, sort and

@@ -18,19 +18,19 @@
 // and k = 8 (l / 16) .. + 7; the result gives lane l the column l % 16 and
 // rows 4 (l / 16) .. + 3.
 //
-// The k loop runs over tiles of 64 k.  The weight tile (128 columns x 64 k,
-// 16 KiB: the bytes that bound the projection, read from HBM once per
-// launch) is loaded once per workgroup, each thread fetching four 16-byte
-// chunks, and stored to LDS, where the four waves read their B fragments;
-// columns are padded to 144 bytes so the 16 lanes reading one k chunk of
-// 16 consecutive columns spread over the banks.  Two LDS buffers alternate
-// (one read by the MFMAs while the next tile is stored to the other, one
-// barrier per tile), and the weight loads run two tiles ahead of the MFMAs
-// in two register sets.  Each wave's x fragments (its own rows, from L2)
-// are loaded one tile ahead.  Measured at 256 x 4096 x 128256: 799 us with
-// each wave loading its own weight fragments, 567 us with the LDS tile, 527
-// us with the reduction below on DPP and the loads two tiles ahead (a
-// plain hipBLASLt GEMM of the same shape, without the epilogue: 336 us).
+// The k loop runs over tiles of 64 k.  A tile's operands, the workgroup's
+// 256 rows of x and its 128 weight columns (the weight bytes bound the
+// projection and are read from HBM once per launch), are loaded once per
+// workgroup, each thread fetching twelve 16-byte chunks, and stored to LDS,
+// where the waves read their A and B fragments; lines are padded to 144
+// bytes so the 16 lanes reading one k chunk of 16 consecutive lines spread
+// over the banks.  Two LDS buffers alternate (one read by the MFMAs while
+// the next tile is stored to the other, one barrier per tile), and the
+// loads run two tiles ahead of the MFMAs in two register sets.  Measured at
+// 256 x 4096 x 128256: 799 us with each wave loading its own fragments, 567
+// us with the weight tile in LDS, 527 us with the reduction below on DPP and
+// the loads two tiles ahead, 459 us with x in LDS too (a plain hipBLASLt
+// GEMM of the same shape, without the epilogue: 336 us).
 //
 // Epilogue: the logits are rounded to bf16 (round to nearest even) and
 // stored, and for every row the largest logit of each 64-column tile is
@@ -70,36 +70,31 @@ __device__ __forceinline__ uint32_t bf16_key(uint32_t b) {
 
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
 
-// Eight bf16 of row `p` from k (zeros where the row or k is out of range).
-__device__ __forceinline__ bf16x8 load8(const uint16_t *base, int64_t ld, int row, int nrows, int k, int K) {
-  if (row < nrows && k < K) {
-    const u32x4v v = *(const u32x4v *)(base + (int64_t)row * ld + k);
-    return __builtin_bit_cast(bf16x8, v);
-  }
-  return __builtin_bit_cast(bf16x8, u32x4v{0u, 0u, 0u, 0u});
-}
-
-// The weight tile of kLhTileK k (kLhCols columns, bf16) in LDS, one
-// 128-byte column every kLhColStride bytes (padded against bank conflicts);
-// two buffers, one filled while the other is read.  A tile holds two MFMA
-// k steps.
+// A k tile: kLhTileK k (two MFMA k steps), one 128-byte line of it per row
+// of x or column of w, stored every kLhColStride bytes in LDS (padded
+// against bank conflicts).
 constexpr int kLhTileK = 2 * kLhStep;
 constexpr int kLhColStride = kLhTileK * 2 + 16;
-constexpr int kLhTileBytes = kLhCols * kLhColStride;
-constexpr int kLhColChunks = kLhTileK / 8;                  // 16-byte chunks of a column
-constexpr int kLhChunks = kLhCols * kLhColChunks;            // 16-byte chunks of a tile
-constexpr int kLhChunksPer = kLhChunks / kLhThreads;        // per thread
-static_assert(kLhChunks % kLhThreads == 0, "tile chunks per thread");
+constexpr int kLhColChunks = kLhTileK / 8;  // 16-byte chunks of a line
+
+// Both operands of a k tile in LDS: the workgroup's kLhRows rows of x, then
+// its kLhCols weight columns, one padded 128-byte line each.
+constexpr int kLhLines = kLhRows + kLhCols;
+constexpr int kLhBufBytes = kLhLines * kLhColStride;
+constexpr int kLhLineChunksPer = kLhLines * kLhColChunks / kLhThreads;  // 16-byte chunks per thread
+constexpr int kLhXChunksPer = kLhRows * kLhColChunks / kLhThreads;      // of which x
+static_assert(kLhLines * kLhColChunks % kLhThreads == 0 && kLhRows * kLhColChunks % kLhThreads == 0, "chunks");
 
 __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restrict__ out, const uint16_t *__restrict__ x,
                                                            const uint16_t *__restrict__ w, int rows, int K, int V,
                                                            uint64_t *__restrict__ tile_max) {
-  __shared__ __attribute__((aligned(16))) unsigned char wt[2][kLhTileBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char tb[2][kLhBufBytes];
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int col0 = (int)blockIdx.x * kLhCols;
-  const int row0 = (int)blockIdx.y * kLhRows + wave * kLhRowsPerWave;
-  const int li = lane & 15, lk = (lane >> 4) * 8;  // operand row/column in a block, k offset
+  const int xrow0 = (int)blockIdx.y * kLhRows;
+  const int row0 = xrow0 + wave * kLhRowsPerWave;
+  const int li = lane & 15;  // operand row/column in a block
 
   f32x4 acc[kLhRB][kLhCB];
 #pragma unroll
@@ -107,71 +102,67 @@ __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restric
 #pragma unroll
     for (int j = 0; j < kLhCB; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // this thread's chunks of the weight tile: column c / kLhColChunks, k chunk
-  // c % kLhColChunks.  Two register sets: the tile two ahead is in flight in
-  // one while the other (the next tile, issued an iteration earlier) lands
-  // and is stored to LDS.  Chunks past K load a clamped address (in bounds:
-  // K > 0 is a multiple of 8) and store zeros; a per-lane guard on the loads
-  // instead cost 75 us at 256 x 4096 x 128256.
-  u32x4v w0[kLhChunksPer], w1[kLhChunksPer];
-  auto fetch_w = [&](int k0, u32x4v (&wr)[kLhChunksPer]) {
+  // this thread's chunks of a tile: line c / kLhColChunks (x rows first),
+  // k chunk c % kLhColChunks.  Two register sets: the tile two ahead is in
+  // flight in one while the other (the next tile, issued an iteration
+  // earlier) lands and is stored to LDS.  Chunks past K or past the last
+  // row / column load a clamped address (in bounds: K > 0 is a multiple of
+  // 8, rows and V are positive) and store zeros.
+  u32x4v s0[kLhLineChunksPer], s1[kLhLineChunksPer];
+  auto fetch = [&](int k0, u32x4v (&st)[kLhLineChunksPer]) {
 #pragma unroll
-    for (int q = 0; q < kLhChunksPer; ++q) {
-      const int c = tid + q * kLhThreads, col = col0 + c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
-      const int cc = col < V ? col : V - 1, kc = k < K ? k : 0;
-      wr[q] = *(const u32x4v *)(w + (int64_t)cc * K + kc);
+    for (int q = 0; q < kLhLineChunksPer; ++q) {
+      const int c = tid + q * kLhThreads, line = c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
+      const int kc = k < K ? k : 0;
+      if (q < kLhXChunksPer) {
+        const int r = xrow0 + line, rc = r < rows ? r : rows - 1;
+        st[q] = *(const u32x4v *)(x + (int64_t)rc * K + kc);
+      } else {
+        const int col = col0 + line - kLhRows, cc = col < V ? col : V - 1;
+        st[q] = *(const u32x4v *)(w + (int64_t)cc * K + kc);
+      }
     }
   };
-  auto store_w = [&](int k0, const u32x4v (&wr)[kLhChunksPer], int buf) {
+  auto store = [&](int k0, const u32x4v (&st)[kLhLineChunksPer], int buf) {
 #pragma unroll
-    for (int q = 0; q < kLhChunksPer; ++q) {
-      const int c = tid + q * kLhThreads, col = col0 + c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
+    for (int q = 0; q < kLhLineChunksPer; ++q) {
+      const int c = tid + q * kLhThreads, line = c / kLhColChunks, k = k0 + (c % kLhColChunks) * 8;
+      const bool in = (q < kLhXChunksPer ? xrow0 + line < rows : col0 + line - kLhRows < V) && k < K;
       const u32x4v z = {0u, 0u, 0u, 0u};
-      *(u32x4v *)&wt[buf][(c / kLhColChunks) * kLhColStride + (c % kLhColChunks) * 16] = (col < V && k < K) ? wr[q] : z;
+      *(u32x4v *)&tb[buf][line * kLhColStride + (c % kLhColChunks) * 16] = in ? st[q] : z;
     }
   };
-  bf16x8 a[2][kLhRB], an[2][kLhRB];
-  auto fetch_x = [&](int k0, bf16x8 (&fa)[2][kLhRB]) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < kLhRB; ++i) fa[h][i] = load8(x, K, row0 + 16 * i + li, rows, k0 + h * kLhStep + lk, K);
+  auto frag = [&](int buf, int line, int h) {
+    return __builtin_bit_cast(bf16x8, *(const u32x4v *)&tb[buf][line * kLhColStride + h * 64 + (lane >> 4) * 16]);
   };
-  // one tile: issue tile t + 2's weights into `wfill` and tile t + 1's x,
-  // run tile t's MFMAs from LDS buffer `buf`, store tile t + 1 (in `wland`)
-  // to the other buffer
-  auto tile = [&](int k0, u32x4v (&wfill)[kLhChunksPer], const u32x4v (&wland)[kLhChunksPer], int buf) {
-    fetch_w(k0 + 2 * kLhTileK, wfill);
-    fetch_x(k0 + kLhTileK, an);
+  // one tile: issue tile t + 2 into `fill`, run tile t's MFMAs from LDS
+  // buffer `buf`, store tile t + 1 (in `land`) to the other buffer
+  auto tile = [&](int k0, u32x4v (&fill)[kLhLineChunksPer], const u32x4v (&land)[kLhLineChunksPer], int buf) {
+    fetch(k0 + 2 * kLhTileK, fill);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      bf16x8 b[kLhCB];
+      bf16x8 av[kLhRB], b[kLhCB];
 #pragma unroll
-      for (int j = 0; j < kLhCB; ++j)
-        b[j] = __builtin_bit_cast(
-            bf16x8, *(const u32x4v *)&wt[buf][(16 * j + li) * kLhColStride + h * 64 + (lane >> 4) * 16]);
+      for (int i = 0; i < kLhRB; ++i) av[i] = frag(buf, wave * kLhRowsPerWave + 16 * i + li, h);
+#pragma unroll
+      for (int j = 0; j < kLhCB; ++j) b[j] = frag(buf, kLhRows + 16 * j + li, h);
 #pragma unroll
       for (int i = 0; i < kLhRB; ++i)
 #pragma unroll
         for (int j = 0; j < kLhCB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h][i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], b[j], acc[i][j], 0, 0, 0);
     }
-    store_w(k0 + kLhTileK, wland, buf ^ 1);
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int i = 0; i < kLhRB; ++i) a[h][i] = an[h][i];
+    store(k0 + kLhTileK, land, buf ^ 1);
     __syncthreads();  // the other buffer is written; this one's reads are done
   };
   if (K > 0) {  // (K = 0: no weight row to clamp to; the logits are zeros)
-    fetch_w(0, w0);
-    fetch_x(0, a);
-    fetch_w(kLhTileK, w1);
-    store_w(0, w0, 0);
+    fetch(0, s0);
+    fetch(kLhTileK, s1);
+    store(0, s0, 0);
     __syncthreads();
     for (int k0 = 0; k0 < K; k0 += 2 * kLhTileK) {
-      tile(k0, w0, w1, 0);
-      if (k0 + kLhTileK < K) tile(k0 + kLhTileK, w1, w0, 1);
+      tile(k0, s0, s1, 0);
+      if (k0 + kLhTileK < K) tile(k0 + kLhTileK, s1, s0, 1);
     }
   }
 
