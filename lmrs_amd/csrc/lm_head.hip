@@ -29,8 +29,9 @@
 // loads run two tiles ahead of the MFMAs in two register sets.  Measured at
 // 256 x 4096 x 128256: 799 us with each wave loading its own fragments, 567
 // us with the weight tile in LDS, 527 us with the reduction below on DPP and
-// the loads two tiles ahead, 459 us with x in LDS too (a plain hipBLASLt
-// GEMM of the same shape, without the epilogue: 336 us).
+// the loads two tiles ahead, 459 us with x in LDS too, 15 us less again
+// with the epilogue below skipping per-element range tests for whole tiles
+// (a plain hipBLASLt GEMM of the same shape, without the epilogue: 336 us).
 //
 // Epilogue: the logits are rounded to bf16 (round to nearest even) and
 // stored, and for every row the largest logit of each 64-column tile is
@@ -168,6 +169,9 @@ __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restric
 
   // Epilogue.  Lane l holds column 16 j + l % 16 and rows 16 i + 4 (l / 16) + q.
   const int ntiles = (V + kTileCols - 1) / kTileCols;
+  // every row and column of this wave's tile in range (the common case): no per-element test
+  const bool whole = row0 + kLhRowsPerWave <= rows && col0 + kLhCols <= V;
+  const uint32_t lowc = 0xFFFFu - (uint32_t)li;  // 0xFFFF - column % 64 in a tile's first block
 #pragma unroll
   for (int i = 0; i < kLhRB; ++i) {
 #pragma unroll
@@ -175,14 +179,25 @@ __global__ void __launch_bounds__(kLhThreads) lm_head_kernel(uint16_t *__restric
       const int row = row0 + 16 * i + 4 * (lane >> 4) + q;
       // per 64-column tile (blocks 0-3 and 4-7): this lane's best of its four columns
       uint32_t best[2] = {0u, 0u};
+      uint16_t *orow = out + (int64_t)row * V + col0 + li;
+      if (whole) {
 #pragma unroll
-      for (int j = 0; j < kLhCB; ++j) {
-        const int col = col0 + 16 * j + li;
-        const uint32_t bits = f32_to_bf16_dev(acc[i][j][q]);
-        if (row < rows && col < V) {
-          out[(int64_t)row * V + col] = (uint16_t)bits;
-          const uint32_t e = (bf16_key(bits) << 16) | (0xFFFFu - (uint32_t)(col % kTileCols));
+        for (int j = 0; j < kLhCB; ++j) {
+          const uint32_t bits = f32_to_bf16_dev(acc[i][j][q]);
+          orow[16 * j] = (uint16_t)bits;
+          const uint32_t e = (bf16_key(bits) << 16) | (lowc - 16u * (uint32_t)(j % 4));
           best[j / 4] = e > best[j / 4] ? e : best[j / 4];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kLhCB; ++j) {
+          const int col = col0 + 16 * j + li;
+          const uint32_t bits = f32_to_bf16_dev(acc[i][j][q]);
+          if (row < rows && col < V) {
+            orow[16 * j] = (uint16_t)bits;
+            const uint32_t e = (bf16_key(bits) << 16) | (0xFFFFu - (uint32_t)(col % kTileCols));
+            best[j / 4] = e > best[j / 4] ? e : best[j / 4];
+          }
         }
       }
       if (tile_max) {
