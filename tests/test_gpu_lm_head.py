@@ -106,6 +106,34 @@ def test_lm_head_special_values_and_ties():
     assert np.array_equal(tm.cpu().numpy().view(np.uint64), standalone_tile_max(yb))
 
 
+def test_lm_head_with_no_hidden_features_writes_zeros():
+    """in_features = 0 through the C-ABI (non-null operand pointers, as a C
+    caller may pass): no operand is read, every logit is +0 and each tile's
+    maximum is its lowest column, ties going to the lower column."""
+    import ctypes
+
+    from lmrs_amd import sampling as S
+
+    rows, V = 3, 130
+    nt = (V + TILE - 1) // TILE
+    dummy_x = torch.zeros(8, dtype=torch.bfloat16, device="cuda")
+    dummy_w = torch.zeros(8, dtype=torch.bfloat16, device="cuda")
+    out = torch.full((rows, V), 7.0, dtype=torch.bfloat16, device="cuda")
+    tm = torch.zeros((rows, nt), dtype=torch.int64, device="cuda")
+    s = torch.cuda.current_stream()
+    print(f"[case] lm_head rows={rows} K=0 V={V}", flush=True)
+    rc = S.lib().lmrs_lm_head_fwd(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(dummy_x.data_ptr()),
+                                  ctypes.c_void_p(dummy_w.data_ptr()), rows, 0, V, S.DTYPE_BF16,
+                                  ctypes.c_void_p(tm.data_ptr()), ctypes.c_void_p(s.cuda_stream))
+    assert rc == S.LMRS_OK
+    torch.cuda.synchronize()
+    yb = out.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.all(yb == 0)
+    expect = standalone_tile_max(yb)
+    assert np.array_equal(tm.cpu().numpy().view(np.uint64), expect)
+    assert np.all(np.uint64(0xFFFFFFFF) - (expect & np.uint64(0xFFFFFFFF)) == np.arange(nt, dtype=np.uint64) * TILE)
+
+
 def test_lm_head_at_the_c3_shape_feeds_the_sampler():
     """rows 256, H 4096, V 128256 (C3's batch and vocab): the fused tile maxima
     equal the standalone statistic on the whole output, sampled logits lie
